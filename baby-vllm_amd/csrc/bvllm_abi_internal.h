@@ -1,0 +1,60 @@
+// Argument blocks passed from the C-ABI entry points to the kernel launchers.
+// All strides are in elements. Tensors are bf16 unless noted.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bvllm {
+
+struct RopeArgs {
+  void* q;        int64_t q_st, q_sh;      // [T, H, D], last-dim stride 1
+  void* k;        int64_t k_st, k_sh;      // [T, Hkv, D]
+  const void* v;  int64_t v_st, v_sh;      // [T, Hkv, D]
+  const void* cos; int64_t cs_st;          // [T, D]
+  const void* sin; int64_t sn_st;          // [T, D]
+  void* k_cache;  int64_t kc_slot, kc_head;  // flat [NB·BS, Hkv, D] view of kv_cache[0]
+  void* v_cache;  int64_t vc_slot, vc_head;  // flat view of kv_cache[1]
+  const int64_t* slot_mapping;             // [T]
+  int64_t num_slots;                       // NB·BS; slots outside [0, num_slots) are not written
+  int32_t num_tokens, num_heads, num_kv_heads, head_dim;
+  int32_t has_cache;
+  int32_t vec_ok;                          // every row start and stride is 16-byte aligned
+};
+
+struct DecodeArgs {
+  const void* q;  int64_t q_sb, q_sh;      // [B, H, D]
+  const void* k_cache; const void* v_cache;  // [NB, BS, Hkv, D] each
+  int64_t c_sb, c_st, c_sh;                // page, token, head strides (shared by K and V)
+  int32_t num_pages;                       // NB; table entries are clamped into [0, NB)
+  const int32_t* block_tables; int64_t bt_stride; int32_t max_blocks;
+  const int32_t* seq_lens;                 // [B]
+  float scale_log2;                        // softmax scale · log2(e)
+  void* out;      int64_t o_sb, o_sh;      // [B, H, D], written when num_splits == 1
+  float* part_out;                         // [B, H, S, D] fp32, when num_splits > 1
+  float* part_lse;                         // [B, H, S] fp32 (log2 units), when num_splits > 1
+  int32_t num_splits, blocks_per_split;
+  int32_t batch, num_heads, num_kv_heads, head_dim;
+  int32_t waves;                           // waves per work-group (4 or 8)
+};
+
+struct PrefillArgs {
+  const void* q;  int64_t q_st, q_sh;      // [T, H, D]
+  const void* k_cache; const void* v_cache;
+  int64_t c_sb, c_st, c_sh;
+  int32_t num_pages;
+  const int32_t* block_tables; int64_t bt_stride; int32_t max_blocks;
+  const int32_t* query_start_loc;          // [S+1]
+  const int32_t* seq_lens;                 // [S]
+  const int32_t* context_lens;             // [S]
+  float scale_log2;
+  void* out;      int64_t o_st, o_sh;      // [T, H, D]
+  int32_t num_seqs, num_tokens, max_query_len;
+  int32_t num_heads, num_kv_heads, head_dim;
+};
+
+hipError_t rope_kv_append(const RopeArgs& a, hipStream_t stream);
+hipError_t paged_decode(const DecodeArgs& a, hipStream_t stream);
+hipError_t paged_prefill(const PrefillArgs& a, hipStream_t stream);
+
+}  // namespace bvllm

@@ -1,0 +1,137 @@
+/*
+ * babyvllm_amd — C ABI of the MI355X (gfx950) paged-KV hot path.
+ *
+ * Three operations, each a drop-in for one Python entry point of the
+ * reference's babyvllm/kernels package:
+ *
+ *   bvllm_rope_kv_append  <- fused_rope_and_cache      (babyvllm/kernels/rope.py:101-153)
+ *   bvllm_paged_decode    <- paged_decode_attention    (babyvllm/kernels/paged_attn.py:259-346)
+ *   bvllm_paged_prefill   <- paged_prefill_attention   (babyvllm/kernels/paged_prefill.py:104-146)
+ *
+ * Conventions shared by every entry point:
+ *   - Tensors are device pointers to bf16 (uint16 bit patterns) unless noted;
+ *     strides are in ELEMENTS; the last (head_dim) stride is always 1.
+ *   - The KV cache of one layer is the reference's [2, num_blocks, block_size,
+ *     num_kv_heads, head_dim] tensor (babyvllm/worker/model_runner.py:224-239);
+ *     k_cache = &cache[0], v_cache = &cache[1], and the page / token / head
+ *     strides are those of cache[0] (cache[1] must have the same).
+ *   - block_size must be 16; head_dim must be 64 or 128 (RoPE also takes 256);
+ *     num_heads must be a multiple of num_kv_heads with a ratio of at most 16.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream). Every call is
+ *     asynchronous, does no host<->device copy and no host synchronisation, and
+ *     allocates nothing, so it may be captured in a hipGraph.
+ *   - Returns 0 on success, otherwise a hipError_t value
+ *     (hipErrorInvalidValue = 1 for rejected arguments); bvllm_error_string
+ *     turns it into text.
+ *   - Table entries outside [0, num_blocks) are clamped into the pool and
+ *     slots outside [0, num_blocks*block_size) are not written (the reference
+ *     would access memory outside the cache in both cases).
+ */
+#ifndef BABYVLLM_AMD_H
+#define BABYVLLM_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI version of this header; bumped on any signature change. */
+#define BVLLM_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define BVLLM_API __attribute__((visibility("default")))
+#else
+#define BVLLM_API
+#endif
+
+BVLLM_API int bvllm_abi_version(void);
+
+/* Text for a return code of this library. */
+BVLLM_API const char* bvllm_error_string(int code);
+
+/*
+ * Fused RoPE + KV-store append. Replaces fused_rope_and_cache
+ * (babyvllm/kernels/rope.py:101-153, kernel rope.py:5-98).
+ *
+ * Rotates q [T, H, D] and k [T, Hkv, D] in place with rotate-half RoPE:
+ *   x[:D/2] <- x[:D/2]·cos[:D/2] − x[D/2:]·sin[:D/2]
+ *   x[D/2:] <- x[D/2:]·cos[D/2:] + x[:D/2]·sin[D/2:]
+ * each product and the sum rounded to bf16 (torch's eager bf16 ops).
+ * If k_cache is non-NULL, writes the rotated k and the raw v [T, Hkv, D] into
+ * the cache row of slot_mapping[t] (int64 [T]); slot = page·16 + offset.
+ * cos/sin are [T, D] bf16 rows (one per token).
+ */
+BVLLM_API int bvllm_rope_kv_append(void* q, int64_t q_stride_t, int64_t q_stride_h,
+                         void* k, int64_t k_stride_t, int64_t k_stride_h,
+                         const void* v, int64_t v_stride_t, int64_t v_stride_h,
+                         const void* cos, int64_t cos_stride_t,
+                         const void* sin, int64_t sin_stride_t,
+                         void* k_cache, void* v_cache,
+                         int64_t cache_stride_slot, int64_t cache_stride_head,
+                         int64_t num_slots, const int64_t* slot_mapping,
+                         int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                         int32_t head_dim, void* stream);
+
+/*
+ * Bytes of fp32 scratch bvllm_paged_decode needs for a split launch:
+ * part_out [B, H, S, D] followed by part_lse [B, H, S] (the reference's
+ * part_out / part_lse, babyvllm/kernels/paged_attn.py:317-318). 0 when num_splits <= 1.
+ */
+BVLLM_API int64_t bvllm_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_splits,
+                                     int32_t head_dim);
+
+/*
+ * Paged decode attention, one query token per sequence. Replaces
+ * paged_decode_attention + _split_decode_attention (babyvllm/kernels/paged_attn.py:259-346)
+ * and its three kernels (paged_attn.py:9-251).
+ *
+ * q [B, H, D]; block_tables int32 [B, >= max_blocks] (row stride bt_stride);
+ * seq_lens int32 [B]; out [B, H, D] bf16. Row b attends keys 0..seq_lens[b]-1
+ * (at most max_blocks pages); a row with seq_len 0 outputs zeros.
+ * (num_splits, blocks_per_split) is the flash-decoding plan
+ * (decode_split_plan, babyvllm/kernels/decode_split.py:48-79): split s covers
+ * pages [s·bps, (s+1)·bps), the last split runs to the row's last page.
+ * num_splits > 1 needs `workspace` of bvllm_decode_workspace_bytes() bytes.
+ * `waves` (0 = choose) is the number of 64-lane waves per work-group; it must
+ * be the same for launches whose bits are compared.
+ */
+BVLLM_API int bvllm_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                       const void* k_cache, const void* v_cache,
+                       int64_t cache_stride_block, int64_t cache_stride_tok, int64_t cache_stride_head,
+                       int32_t num_blocks,
+                       const int32_t* block_tables, int64_t bt_stride, int32_t max_blocks,
+                       const int32_t* seq_lens, float scale,
+                       void* out, int64_t out_stride_b, int64_t out_stride_h,
+                       void* workspace, int32_t num_splits, int32_t blocks_per_split,
+                       int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                       int32_t head_dim, int32_t block_size, int32_t waves, void* stream);
+
+/*
+ * Varlen paged prefill attention. Replaces paged_prefill_attention
+ * (babyvllm/kernels/paged_prefill.py:104-146, kernel :6-101).
+ *
+ * q [T, H, D] holds the query rows of num_seqs sequences back to back:
+ * sequence s owns rows query_start_loc[s] .. query_start_loc[s+1]-1 (int32 [S+1]).
+ * Row i of sequence s sits at position context_lens[s] + i and attends keys
+ * 0 .. context_lens[s] + i (and < seq_lens[s]) read from the cache through
+ * block_tables[s]. K/V of the new tokens must already be in the cache.
+ * max_query_len bounds every sequence's query count (it sizes the grid).
+ */
+BVLLM_API int bvllm_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                        const void* k_cache, const void* v_cache,
+                        int64_t cache_stride_block, int64_t cache_stride_tok, int64_t cache_stride_head,
+                        int32_t num_blocks,
+                        const int32_t* block_tables, int64_t bt_stride, int32_t max_blocks,
+                        const int32_t* query_start_loc, const int32_t* seq_lens,
+                        const int32_t* context_lens, float scale,
+                        void* out, int64_t out_stride_t, int64_t out_stride_h,
+                        int32_t num_seqs, int32_t num_tokens, int32_t max_query_len,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                        int32_t block_size, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BABYVLLM_AMD_H */

@@ -1,0 +1,309 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the GPU kernels' checker.
+
+The reference ships no stored vectors for this path (its tests draw seeded
+random inputs and compare against its torch path). Each oracle function is
+therefore pinned by something a plausible mistake would fail:
+  * closed forms that do not reuse the oracle's formula (complex rotation for
+    RoPE, IEEE round-to-nearest-even on raw bits for bf16 rounding, explicit
+    slot arithmetic for the scatter),
+  * independent float64 brute force on small inputs (attention),
+  * textbook/library special cases (G = 1 is plain MHA; ctx = 0 is causal SDPA;
+    one decode token is the last row of a full causal prefill; identical keys
+    give the mean of V; a single key returns its V),
+  * the reference's own behaviour tests and known answers, ported
+    (tests/test_attention.py:16-298, tests/test_prefix_caching.py:133-164,
+    tests/test_decode_inputs.py:113-150).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as oa
+from oracle import rope as orope
+
+
+class MD:
+    """Minimal AttentionMetadata stand-in (fields of babyvllm/worker/context.py:5-17)."""
+
+    def __init__(self, block_tables, qsl, seq_lens, ctx_lens):
+        self.block_tables = torch.tensor(block_tables, dtype=torch.int32)
+        self.query_start_loc_cpu = list(qsl)
+        self.seq_lens_cpu = list(seq_lens)
+        self.context_lens_cpu = list(ctx_lens)
+        self.query_start_loc = torch.tensor(qsl, dtype=torch.int32)
+        self.seq_lens = torch.tensor(seq_lens, dtype=torch.int32)
+        self.context_lens = torch.tensor(ctx_lens, dtype=torch.int32)
+        self.max_query_len = max(b - a for a, b in zip(qsl[:-1], qsl[1:]))
+        self.max_seq_len = max(seq_lens)
+
+
+# --------------------------------------------------------------------- RoPE
+
+def test_rope_tables_match_the_closed_form():
+    D, P, base = 64, 300, 1e6
+    cos, sin = orope.rope_tables(D, P, base)
+    pos = np.arange(P)[:, None].astype(np.float64)
+    i = np.arange(D // 2)[None, :].astype(np.float64)
+    ang = pos * base ** (-2.0 * i / D)
+    np.testing.assert_allclose(cos[:, : D // 2].numpy(), np.cos(ang), atol=2e-4)
+    np.testing.assert_allclose(sin[:, : D // 2].numpy(), np.sin(ang), atol=2e-4)
+    # duplicated halves
+    assert torch.equal(cos[:, : D // 2], cos[:, D // 2:])
+    assert torch.equal(sin[:, : D // 2], sin[:, D // 2:])
+
+
+def test_apply_rope_is_complex_rotation_in_float64():
+    g = torch.Generator().manual_seed(0)
+    T, H, D = 5, 3, 16
+    q = torch.randn(T, H, D, generator=g, dtype=torch.float64)
+    k = torch.randn(T, 2, D, generator=g, dtype=torch.float64)
+    theta = torch.rand(T, D // 2, generator=g, dtype=torch.float64) * 6.0
+    cos = torch.cat([theta.cos(), theta.cos()], -1)
+    sin = torch.cat([theta.sin(), theta.sin()], -1)
+    qr, kr = orope.apply_rope(q, k, cos, sin)
+    for x, xr in ((q, qr), (k, kr)):
+        z = torch.complex(x[..., : D // 2], x[..., D // 2:]) * torch.polar(
+            torch.ones_like(theta), theta)[:, None, :]
+        torch.testing.assert_close(xr[..., : D // 2], z.real, atol=1e-12, rtol=0)
+        torch.testing.assert_close(xr[..., D // 2:], z.imag, atol=1e-12, rtol=0)
+
+
+def test_apply_rope_position_zero_is_identity_and_relative_phase_holds():
+    D, base = 32, 1e6
+    cos_t, sin_t = orope.rope_tables(D, 64, base)
+    cos_t, sin_t = cos_t.double(), sin_t.double()
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(1, 1, D, generator=g, dtype=torch.float64)
+    k = torch.randn(1, 1, D, generator=g, dtype=torch.float64)
+    q0, k0 = orope.apply_rope(q, k, cos_t[:1], sin_t[:1])
+    assert torch.equal(q0, q) and torch.equal(k0, k)
+
+    def dot(pq, pk):
+        a, _ = orope.apply_rope(q, q, cos_t[pq:pq + 1], sin_t[pq:pq + 1])
+        b, _ = orope.apply_rope(k, k, cos_t[pk:pk + 1], sin_t[pk:pk + 1])
+        return float((a * b).sum())
+
+    assert math.isclose(dot(10, 3), dot(17, 10), rel_tol=1e-5, abs_tol=1e-5)
+
+
+def test_apply_rope_bf16_rounds_after_each_op():
+    """torch bf16 eager ops == the numpy per-op RNE restatement, bit for bit."""
+    g = torch.Generator().manual_seed(2)
+    T, H, D = 17, 28, 128
+    q = torch.randn(T, H, D, generator=g).bfloat16()
+    k = torch.randn(T, 4, D, generator=g).bfloat16()
+    cos = torch.randn(T, D, generator=g).bfloat16()
+    sin = torch.randn(T, D, generator=g).bfloat16()
+    qr, kr = orope.apply_rope(q, k, cos, sin)
+    for x, xr in ((q, qr), (k, kr)):
+        want = orope.apply_rope_bf16_explicit(x.float().numpy(), cos.float().numpy(), sin.float().numpy())
+        assert np.array_equal(xr.float().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_bf16_round_is_round_to_nearest_even():
+    vals = np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -9, 1.0 + 2 ** -9, -1.0 - 2 ** -9,
+                     3.0e38, np.float32(np.inf)], dtype=np.float32)
+    got = orope.bf16_round_np(vals)
+    want = torch.tensor(vals).bfloat16().float().numpy()
+    assert np.array_equal(got, want)
+    assert got[3] == 1.0  # tie rounds to the even mantissa
+    assert got[2] == 1.0 + 2 ** -7
+
+
+# -------------------------------------------------------------- KV scatter
+
+def test_store_kvcache_places_rows_at_their_slots():
+    g = torch.Generator().manual_seed(3)
+    NB, BS, Hkv, D = 6, 4, 2, 8
+    cache = torch.zeros(2, NB, BS, Hkv, D)
+    slots = torch.tensor([7, 0, 23, 12, 5])
+    k = torch.randn(5, Hkv, D, generator=g)
+    v = torch.randn(5, Hkv, D, generator=g)
+    orope.store_kvcache(k, v, cache, slots)
+    for t, s in enumerate(slots.tolist()):
+        assert torch.equal(cache[0, s // BS, s % BS], k[t])
+        assert torch.equal(cache[1, s // BS, s % BS], v[t])
+    written = set(slots.tolist())
+    for s in range(NB * BS):
+        if s not in written:
+            assert cache[:, s // BS, s % BS].abs().sum() == 0
+
+
+def test_slot_arithmetic_known_answers():
+    # tests/test_decode_inputs.py:146-150 and :113-122 of the reference.
+    assert orope.slot_of([5, 6], 20, 16) == 6 * 16 + 4
+    assert orope.slot_of([3, 9, 1, 4], 50, 16) == 4 * 16 + 2
+
+
+def test_slot_mapping_round_trip_through_the_block_table():
+    """KVCheckingRunner (tests/test_prefix_caching.py:133-164): write by slot, read by table."""
+    bs, n_blocks = 4, 10
+    tables = {0: [7, 2, 5], 1: [0, 9], 2: [3]}
+    tokens = {0: list(range(100, 111)), 1: list(range(200, 206)), 2: [300, 301]}
+    pool = [None] * (n_blocks * bs)
+    for s, toks in tokens.items():
+        for p, tok in enumerate(toks):
+            pool[orope.slot_of(tables[s], p, bs)] = tok
+    for s, toks in tokens.items():
+        back = [pool[tables[s][p // bs] * bs + p % bs] for p in range(len(toks))]
+        assert back == toks
+
+
+# ------------------------------------------------------------ attention
+
+def _paged_case(lens, hkv, g_, d, bs=4, seed=0, dtype=torch.float64):
+    gen = torch.Generator().manual_seed(seed)
+    width = max(-(-n // bs) for n in lens) + 1
+    total = len(lens) * width + 1
+    cache = torch.randn(2, total, bs, hkv, d, generator=gen, dtype=dtype)
+    bt = torch.randperm(total, generator=gen)[: len(lens) * width].view(len(lens), width).int()
+    q = torch.randn(len(lens), hkv * g_, d, generator=gen, dtype=dtype)
+    return q, cache, bt
+
+
+@pytest.mark.parametrize("hkv,g_", [(2, 3), (1, 1), (2, 7)])
+def test_static_decode_matches_brute_force(hkv, g_):
+    lens = [1, 5, 9, 12]
+    q, cache, bt = _paged_case(lens, hkv, g_, 8)
+    scale = 8 ** -0.5
+    got = oa.static_decode_attention(q, cache, bt, torch.tensor(lens, dtype=torch.int32), 12, scale)
+    want = oa.brute_decode(q, cache, bt, lens, scale)
+    torch.testing.assert_close(got, want, atol=1e-10, rtol=0)
+
+
+def test_decode_with_bucket_wider_than_rows_matches_brute_force():
+    lens = [3, 7]
+    q, cache, bt = _paged_case(lens, 2, 2, 8)
+    scale = 0.3
+    got = oa.static_decode_attention(q, cache, bt, torch.tensor(lens, dtype=torch.int32), 8, scale)
+    torch.testing.assert_close(got, oa.brute_decode(q, cache, bt, lens, scale), atol=1e-10, rtol=0)
+
+
+def test_paged_attention_torch_matches_brute_force_mixed_batch():
+    gen = torch.Generator().manual_seed(4)
+    hkv, g_, d, bs = 2, 3, 8, 4
+    specs = [(0, 5), (3, 1), (6, 4), (2, 2)]  # (context, new queries)
+    seq_lens = [c + n for c, n in specs]
+    width = max(-(-s // bs) for s in seq_lens)
+    total = len(specs) * width + 2
+    perm = torch.randperm(total, generator=gen).tolist()
+    tables = [[perm.pop() for _ in range(width)] for _ in specs]
+    cache = torch.randn(2, total, bs, hkv, d, generator=gen, dtype=torch.float64)
+    qsl = [0]
+    for _, n in specs:
+        qsl.append(qsl[-1] + n)
+    q = torch.randn(qsl[-1], hkv * g_, d, generator=gen, dtype=torch.float64)
+    md = MD(tables, qsl, seq_lens, [c for c, _ in specs])
+    scale = d ** -0.5
+    got = oa.paged_attention_torch(q, cache, md, scale, g_)
+    torch.testing.assert_close(got, oa.brute_prefill(q, cache, md, scale), atol=1e-10, rtol=0)
+
+
+def test_gqa_group_of_one_is_plain_mha():
+    gen = torch.Generator().manual_seed(5)
+    T, H, D = 6, 3, 8
+    q, k, v = (torch.randn(T, H, D, generator=gen, dtype=torch.float64) for _ in range(3))
+    got = oa.naive_causal_attention(q, k, v, 0.4, 1)
+    mask = torch.ones(T, T, dtype=torch.bool).tril()
+    s = torch.einsum("thd,shd->hts", q, k) * 0.4
+    s = s.masked_fill(~mask, float("-inf"))
+    want = torch.einsum("hts,shd->thd", s.softmax(-1), v)
+    torch.testing.assert_close(got, want, atol=1e-12, rtol=0)
+
+
+def test_naive_matches_grouped_query_reference():
+    # tests/test_attention.py:224-239 of the reference.
+    q = torch.randn(8, 4, 16, dtype=torch.float64)
+    k = torch.randn(8, 2, 16, dtype=torch.float64)
+    v = torch.randn(8, 2, 16, dtype=torch.float64)
+    ref = F.scaled_dot_product_attention(
+        q.transpose(0, 1), k.repeat_interleave(2, dim=1).transpose(0, 1),
+        v.repeat_interleave(2, dim=1).transpose(0, 1), is_causal=True, scale=0.25,
+    ).transpose(0, 1)
+    torch.testing.assert_close(oa.naive_causal_attention(q, k, v, 0.25, 2), ref, atol=1e-12, rtol=0)
+
+
+def test_one_decode_token_is_the_last_row_of_full_prefill():
+    # tests/test_attention.py:16-55 of the reference.
+    gen = torch.Generator().manual_seed(6)
+    H, Hkv, D, bs = 4, 2, 16, 4
+    q_all = torch.randn(11, H, D, generator=gen, dtype=torch.float64)
+    k_all = torch.randn(11, Hkv, D, generator=gen, dtype=torch.float64)
+    v_all = torch.randn(11, Hkv, D, generator=gen, dtype=torch.float64)
+    expected = oa.naive_causal_attention(q_all, k_all, v_all, D ** -0.5, 2)
+    cache = torch.zeros(2, 3, bs, Hkv, D, dtype=torch.float64)
+    orope.store_kvcache(k_all, v_all, cache, torch.arange(11))
+    got = oa.static_decode_attention(q_all[10:11], cache, torch.tensor([[0, 1, 2]], dtype=torch.int32),
+                                     torch.tensor([11], dtype=torch.int32), 11, D ** -0.5)
+    torch.testing.assert_close(got[0], expected[10], atol=1e-12, rtol=0)
+    md = MD([[0, 1, 2]], [0, 1], [11], [10])
+    got2 = oa.paged_attention_torch(q_all[10:11], cache, md, D ** -0.5, 2)
+    torch.testing.assert_close(got2[0], expected[10], atol=1e-12, rtol=0)
+
+
+def test_identical_keys_average_the_values_and_one_key_returns_its_value():
+    D, Hkv, G = 8, 1, 2
+    cache = torch.zeros(2, 2, 4, Hkv, D, dtype=torch.float64)
+    cache[0] = 0.7  # every key identical -> uniform weights
+    cache[1] = torch.arange(2 * 4 * D, dtype=torch.float64).view(2, 4, 1, D)
+    q = torch.randn(2, G, D, dtype=torch.float64)
+    bt = torch.tensor([[0, 1], [1, 0]], dtype=torch.int32)
+    got = oa.static_decode_attention(q, cache, bt, torch.tensor([6, 1], dtype=torch.int32), 8, 0.5)
+    flat_v = cache[1].reshape(-1, D)
+    torch.testing.assert_close(got[0, 0], flat_v[:6].mean(0), atol=1e-12, rtol=0)
+    torch.testing.assert_close(got[1, 1], cache[1, 1, 0, 0], atol=1e-12, rtol=0)
+
+
+def test_prefill_with_cached_prefix_hides_nothing_of_the_prefix():
+    # tests/test_attention.py:109-180 (batched mixed) of the reference, float64.
+    gen = torch.Generator().manual_seed(7)
+    H, Hkv, D, bs = 4, 2, 16, 4
+    cache = torch.zeros(2, 6, bs, Hkv, D, dtype=torch.float64)
+    q0 = torch.randn(5, H, D, generator=gen, dtype=torch.float64)
+    k0 = torch.randn(5, Hkv, D, generator=gen, dtype=torch.float64)
+    v0 = torch.randn(5, Hkv, D, generator=gen, dtype=torch.float64)
+    orope.store_kvcache(k0, v0, cache, torch.arange(5))
+    kc = torch.randn(4, Hkv, D, generator=gen, dtype=torch.float64)
+    vc = torch.randn(4, Hkv, D, generator=gen, dtype=torch.float64)
+    q1 = torch.randn(1, H, D, generator=gen, dtype=torch.float64)
+    orope.store_kvcache(kc, vc, cache, torch.arange(8, 12))
+    md = MD([[0, 1], [2, 0]], [0, 5, 6], [5, 4], [0, 3])
+    got = oa.paged_attention_torch(torch.cat([q0, q1]), cache, md, D ** -0.5, 2)
+    torch.testing.assert_close(got[:5], oa.naive_causal_attention(q0, k0, v0, D ** -0.5, 2),
+                               atol=1e-12, rtol=0)
+    exp1 = oa.naive_causal_attention(torch.cat([torch.zeros(3, H, D, dtype=torch.float64), q1]),
+                                     kc, vc, D ** -0.5, 2)
+    torch.testing.assert_close(got[5], exp1[3], atol=1e-12, rtol=0)
+
+
+# ------------------------------------------------------- split + LSE merge
+
+@pytest.mark.parametrize("partition", [1, 2, 3, 7])
+def test_lse_merge_of_split_partials_is_the_full_softmax(partition):
+    lens = [1, 17, 40, 0, 33]
+    gen = torch.Generator().manual_seed(8)
+    hkv, g_, d, bs = 2, 3, 8, 16
+    width = 4
+    total = len(lens) * width + 1
+    cache = torch.randn(2, total, bs, hkv, d, generator=gen, dtype=torch.float64)
+    bt = torch.randperm(total, generator=gen)[: len(lens) * width].view(len(lens), width).int()
+    q = torch.randn(len(lens), hkv * g_, d, generator=gen, dtype=torch.float64)
+    splits = -(-width // partition)
+    po, pl = oa.split_partials(q, cache, bt, torch.tensor(lens), 0.35, splits, partition)
+    merged = oa.lse_merge(po, pl)
+    want = oa.brute_decode(q, cache, bt, lens, 0.35)
+    torch.testing.assert_close(merged.double(), want, atol=1e-6, rtol=0)
+    assert merged[3].abs().max() == 0  # padded row: every split empty -> zeros
+
+
+def test_lse_merge_ignores_trailing_empty_splits_bitwise():
+    gen = torch.Generator().manual_seed(9)
+    po = torch.randn(3, 4, 5, 8, generator=gen)
+    pl = torch.randn(3, 4, 5, generator=gen)
+    pad_o = torch.cat([po, torch.zeros(3, 4, 3, 8)], dim=2)
+    pad_l = torch.cat([pl, torch.full((3, 4, 3), float("-inf"))], dim=2)
+    assert torch.equal(oa.lse_merge(po, pl), oa.lse_merge(pad_o, pad_l))

@@ -1,0 +1,186 @@
+"""Paged decode attention: HIP kernel vs the CPU oracle (ports tests/test_paged_attn.py).
+
+Oracle: oracle.attention.static_decode_attention (the reference's gather + SDPA
+decode, babyvllm/layers/attention.py:113-134) in float32 on the CPU, and the
+float64 split/LSE restatement for the split invariants.
+"""
+
+import pytest
+import torch
+
+from oracle import attention as oa
+from tests._cases import BLOCK_SIZE, assert_attn_close, cdiv, make_decode_inputs
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a ROCm GPU"),
+]
+
+HEAD_DIM = 128
+GRAPH_TABLE_WIDTH = 129  # 2048 / 16 + 1
+
+
+def _kernel():
+    from babyvllm.kernels.paged_attn import paged_decode_attention
+    return paged_decode_attention
+
+
+def _oracle(q, kv_cache, bt, lens, scale, bucket=None):
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    bucket = bucket or max(max(lens), 1)
+    out = oa.static_decode_attention(q.float().cpu(), kv_cache.float().cpu(), bt.cpu(), lens_t,
+                                     bucket, scale)
+    return out
+
+
+def _live(lens):
+    return [i for i, n in enumerate(lens) if n > 0]
+
+
+@pytest.mark.parametrize("B", [1, 2, 7, 64])
+@pytest.mark.parametrize("seq_len", [1, 15, 16, 17, 31, 32, 127, 128, 2048])
+def test_paged_decode_parity(B, seq_len):
+    scale = HEAD_DIM ** -0.5
+    q, kv_cache, bt, seq_lens = make_decode_inputs([seq_len] * B, seed=B * 10000 + seq_len)
+    actual = _kernel()(q, kv_cache, bt, seq_lens, scale)
+    assert_attn_close(actual, _oracle(q, kv_cache, bt, [seq_len] * B, scale))
+
+
+RAGGED = [1, 17, 300, 2048, 0, 64, 1000, 16]
+
+
+@pytest.mark.parametrize("partition", [0, 1, 2, 3, 7, 8, 64])
+def test_split_decode_matches_reference_on_ragged_batch(partition):
+    scale = HEAD_DIM ** -0.5
+    q, kv_cache, bt, seq_lens = make_decode_inputs(RAGGED, width=GRAPH_TABLE_WIDTH)
+    actual = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=2048, partition_blocks=partition)
+    assert_attn_close(actual, _oracle(q, kv_cache, bt, RAGGED, scale), rows=_live(RAGGED))
+    assert actual[RAGGED.index(0)].abs().max() == 0
+
+
+@pytest.mark.parametrize("n", [1, 15, 16, 17, 127, 128, 129, 255, 256, 1023, 2047, 2048])
+def test_auto_split_with_bucket_wider_than_live_length(n, monkeypatch):
+    from babyvllm.kernels.decode_split import DECODE_PARTITION_ENV, decode_split_plan
+
+    monkeypatch.delenv(DECODE_PARTITION_ENV, raising=False)
+    scale = HEAD_DIM ** -0.5
+    q, kv_cache, bt, seq_lens = make_decode_inputs([n], width=GRAPH_TABLE_WIDTH, seed=n)
+    sms = torch.cuda.get_device_properties(0).multi_processor_count
+    splits, _ = decode_split_plan(1, 4, BLOCK_SIZE, GRAPH_TABLE_WIDTH, 2048, sms)
+    assert splits > 1
+    actual = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=2048)
+    assert_attn_close(actual, _oracle(q, kv_cache, bt, [n], scale))
+
+
+def test_live_length_and_graph_bucket_give_identical_bits(monkeypatch):
+    from babyvllm.kernels.decode_split import DECODE_PARTITION_ENV
+
+    monkeypatch.delenv(DECODE_PARTITION_ENV, raising=False)
+    scale = HEAD_DIM ** -0.5
+    lens = [300, 17, 129, 0, 5]
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, width=GRAPH_TABLE_WIDTH)
+    eager = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=max(lens))
+    graph = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=2048)
+    assert torch.equal(eager, graph)
+
+
+@pytest.mark.parametrize("n", [1, 17, 63, 64])
+def test_row_within_one_partition_matches_single_pass_bits(n):
+    from babyvllm.kernels.decode_split import auto_partition_blocks
+
+    partition = auto_partition_blocks(2)
+    assert n <= partition * BLOCK_SIZE
+    scale = HEAD_DIM ** -0.5
+    q, kv_cache, bt, seq_lens = make_decode_inputs([n, n], width=GRAPH_TABLE_WIDTH, seed=n)
+    single = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=2048, partition_blocks=0)
+    split = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=2048, partition_blocks=partition)
+    assert torch.equal(single, split)
+
+
+def test_row_longer_than_the_bucket_is_attended_in_full():
+    scale = HEAD_DIM ** -0.5
+    lens = [1000, 40]
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens)
+    actual = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=256, partition_blocks=4)
+    assert_attn_close(actual, _oracle(q, kv_cache, bt, lens, scale))
+
+
+@pytest.mark.parametrize("partition_env", ["0", "auto"])
+def test_decode_attention_replays_in_a_hip_graph(partition_env, monkeypatch):
+    """Grid frozen at capture; lengths, tables and q change between replays."""
+    from babyvllm.kernels.decode_split import DECODE_PARTITION_ENV
+
+    monkeypatch.setenv(DECODE_PARTITION_ENV, partition_env)
+    scale = HEAD_DIM ** -0.5
+    q, kv_cache, bt, seq_lens = make_decode_inputs([2048, 2048, 0, 0], width=GRAPH_TABLE_WIDTH)
+    run = lambda: _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=2048)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = run()
+
+    g = torch.Generator(device="cuda").manual_seed(7)
+    for lens in ([5, 2048, 0, 0], [1999, 33, 129, 0], [1, 1, 1, 1], [5, 2048, 0, 0]):
+        seq_lens.copy_(torch.tensor(lens, dtype=torch.int32))
+        bt.copy_(torch.randperm(bt.numel(), device="cuda", generator=g).view_as(bt).to(torch.int32))
+        q.copy_(torch.randn(q.shape, device="cuda", dtype=q.dtype, generator=g))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = run()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        assert_attn_close(out, _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
+        for i, n in enumerate(lens):
+            if n == 0:
+                assert out[i].abs().max() == 0
+
+
+def test_unwritten_nan_slots_past_seq_len_do_not_leak():
+    scale = HEAD_DIM ** -0.5
+    lens = [17, 33, 5]
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, seed=3)
+    clean = kv_cache.clone()
+    for i, n in enumerate(lens):
+        page = bt[i, (n - 1) // BLOCK_SIZE].item()
+        kv_cache[:, page, n % BLOCK_SIZE or BLOCK_SIZE:] = float("nan")
+        clean[:, page, n % BLOCK_SIZE or BLOCK_SIZE:] = 0
+    for part in (0, 1):
+        actual = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=64, partition_blocks=part)
+        assert_attn_close(actual, _oracle(q, clean, bt, lens, scale))
+
+
+@pytest.mark.parametrize("hkv,group,d", [(2, 7, 64), (4, 1, 64), (1, 16, 128), (8, 4, 128)])
+def test_other_head_configs(hkv, group, d):
+    lens = [1, 40, 200, 513]
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, hkv=hkv, group=group, d=d, seed=11)
+    for part in (0, None, 3):
+        actual = _kernel()(q, kv_cache, bt, seq_lens, d ** -0.5, max_seq_len=520, partition_blocks=part)
+        assert_attn_close(actual, _oracle(q, kv_cache, bt, lens, d ** -0.5))
+
+
+def test_strided_q_view_into_fused_qkv():
+    lens = [100, 7]
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, seed=5)
+    B, H, D = q.shape
+    qkv = torch.randn(B, (H + 8) * D, device="cuda", dtype=q.dtype)
+    view = qkv[:, : H * D].view(B, H, D)
+    view.copy_(q)
+    assert not view.is_contiguous()
+    assert torch.equal(_kernel()(view, kv_cache, bt, seq_lens, D ** -0.5),
+                       _kernel()(q, kv_cache, bt, seq_lens, D ** -0.5))
+
+
+# ---------------------------------------------------- BASELINE config 3 shapes
+
+@pytest.mark.parametrize("batch,ctx", [(64, 1920), (8, 1920), (1, 32768)])
+def test_baseline_decode_configs(batch, ctx):
+    scale = HEAD_DIM ** -0.5
+    lens = [ctx] * batch
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, width=cdiv(ctx, BLOCK_SIZE), seed=ctx + batch)
+    actual = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=ctx)
+    assert_attn_close(actual, _oracle(q, kv_cache, bt, lens, scale))

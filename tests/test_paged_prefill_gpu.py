@@ -1,0 +1,108 @@
+"""Varlen paged prefill attention: HIP kernel vs the CPU oracle (ports tests/test_paged_prefill.py).
+
+Oracle: oracle.attention.paged_attention_torch (the reference's per-sequence
+SDPA loop, babyvllm/layers/attention.py:137-175) in float32 on the CPU, with
+the NaN-filled unwritten slots replaced by zeros for the oracle only.
+"""
+
+import pytest
+import torch
+
+from oracle import attention as oa
+from tests._cases import assert_attn_close, build_prefill_case, md_to_cpu
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a ROCm GPU"),
+]
+
+
+def _kernel():
+    from babyvllm.kernels.paged_prefill import paged_prefill_attention
+    return paged_prefill_attention
+
+
+def _oracle(q, kv_cache, md, group):
+    scale = q.shape[-1] ** -0.5
+    cache = torch.nan_to_num(kv_cache.float().cpu(), nan=0.0)
+    return oa.paged_attention_torch(q.float().cpu(), cache, md_to_cpu(md), scale, group)
+
+
+CASES = {
+    "fresh_prefill": [(0, 128)],
+    "fresh_prefill_ragged": [(0, 1), (0, 17), (0, 100), (0, 64)],
+    "prefix_hit_aligned": [(32, 5), (48, 77), (16, 2)],
+    "prefix_unaligned": [(37, 20), (5, 3), (100, 130)],
+    "mixed_prefill_and_decode": [(0, 40), (200, 1), (63, 1), (500, 1)],
+    "long_tail_after_prefix": [(1024, 1024)],
+    "batch64_fresh": [(0, 128)] * 64,
+}
+
+
+@pytest.mark.parametrize("case", list(CASES))
+@pytest.mark.parametrize("hkv,group,d", [(4, 7, 128), (2, 7, 64), (4, 1, 64)])
+def test_paged_prefill_matches_oracle(case, hkv, group, d):
+    q, kv_cache, md = build_prefill_case(CASES[case], hkv, group, d)
+    expected = _oracle(q, kv_cache, md, group)
+    actual = _kernel()(q, kv_cache, md, d ** -0.5)
+    assert not torch.isnan(actual).any()
+    assert_attn_close(actual, expected)
+
+
+def test_non_contiguous_query_view():
+    hkv, group, d = 4, 7, 128
+    q, kv_cache, md = build_prefill_case([(16, 33), (0, 70)], hkv, group, d)
+    H = hkv * group
+    qkv = torch.randn(q.shape[0], (H + 2 * hkv) * d, device="cuda", dtype=q.dtype)
+    view = qkv[:, : H * d].view(-1, H, d)
+    view.copy_(q)
+    assert not view.is_contiguous()
+    assert_attn_close(_kernel()(view, kv_cache, md, d ** -0.5), _oracle(q, kv_cache, md, group))
+
+
+def test_attention_layer_routes_to_the_hip_kernels(monkeypatch):
+    from babyvllm.layers.attention import Attention
+    from babyvllm.worker.context import set_forward_context
+    import babyvllm.kernels.paged_attn as pa
+    import babyvllm.kernels.paged_prefill as pp
+
+    hkv, group, d = 4, 7, 128
+    q, kv_cache, md = build_prefill_case([(32, 9), (0, 20)], hkv, group, d)
+    attn = Attention(hkv * group, d, hkv)
+    attn.kv_cache = kv_cache
+    calls = []
+    real_p, real_d = pp.paged_prefill_attention, pa.paged_decode_attention
+    monkeypatch.setattr(pp, "paged_prefill_attention", lambda *a: calls.append("prefill") or real_p(*a))
+    monkeypatch.setattr(pa, "paged_decode_attention",
+                        lambda *a, **kw: calls.append("decode") or real_d(*a, **kw))
+    with set_forward_context(md):
+        out = attn(q, q, q)
+    assert calls == ["prefill"]
+    assert_attn_close(out, _oracle(q, kv_cache, md, group))
+
+    q1, kv1, md1 = build_prefill_case([(40, 1), (7, 1)], hkv, group, d, nan_fill=False)
+    attn.kv_cache = kv1
+    with set_forward_context(md1):
+        out1 = attn(q1, q1, q1)
+    assert calls == ["prefill", "decode"]
+    assert_attn_close(out1, _oracle(q1, kv1, md1, group))
+
+
+def test_empty_step_returns_empty():
+    q, kv_cache, md = build_prefill_case([(0, 3)], 4, 7, 128)
+    out = _kernel()(q[:0], kv_cache, md, 0.1)
+    assert out.shape == (0, 28, 128)
+
+
+# ---------------------------------------------------- BASELINE config 4 shapes
+
+@pytest.mark.parametrize("name,specs", [
+    ("64x128_fresh", [(0, 128)] * 64),
+    ("8x(1024+128)", [(1024, 128)] * 8),
+    ("1x(2048+4096)", [(2048, 4096)]),
+    ("1x512+63x(1000+1)", [(0, 512)] + [(1000, 1)] * 63),
+])
+def test_baseline_prefill_configs(name, specs):
+    q, kv_cache, md = build_prefill_case(specs, 4, 7, 128, seed=len(specs))
+    actual = _kernel()(q, kv_cache, md, 128 ** -0.5)
+    assert_attn_close(actual, _oracle(q, kv_cache, md, 7))
