@@ -36,7 +36,7 @@ SIGNATURES = {
         _i32, _i32, _i32, _i32,     # T, H, Hkv, D
         _p,                         # stream
     ]),
-    "bvllm_decode_workspace_bytes": (ctypes.c_int64, [_i32, _i32, _i32, _i32]),
+    "bvllm_decode_workspace_bytes": (ctypes.c_int64, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "bvllm_paged_decode": (ctypes.c_int, [
         _p, _i64, _i64,             # q
         _p, _p, _i64, _i64, _i64,   # caches + strides
@@ -61,7 +61,7 @@ SIGNATURES = {
     ]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class KernelLibraryError(RuntimeError):

@@ -21,10 +21,9 @@ import os
 import torch
 
 from babyvllm.kernels import _lib
-from babyvllm.kernels.decode_split import auto_partition_blocks, decode_split_plan
+from babyvllm.kernels.decode_split import decode_split_plan
 
-# Waves per decode work-group: "auto" or 4 / 8. The value must not depend on
-# the context bucket (bits are compared across buckets), only on the batch.
+# Waves per decode work-group: "auto" (the library's choice) or 8.
 DECODE_WAVES_ENV = "BVLLM_DECODE_WAVES"
 
 
@@ -33,12 +32,10 @@ def _num_sms(device_index: int) -> int:
     return torch.cuda.get_device_properties(device_index).multi_processor_count
 
 
-def decode_waves(batch: int) -> int:
-    """Waves per work-group for a batch: a function of the batch bucket only."""
+def decode_waves() -> int:
+    """Waves per work-group to request: 0 lets the library choose."""
     setting = os.environ.get(DECODE_WAVES_ENV, "auto")
-    if setting != "auto":
-        return int(setting)
-    return 4 if auto_partition_blocks(batch) <= 4 else 8
+    return 0 if setting == "auto" else int(setting)
 
 
 def _device_index(t: torch.Tensor) -> int:
@@ -84,8 +81,9 @@ def paged_decode_attention(q, kv_cache, block_tables, seq_lens, scale,
     if B == 0:
         return out
     workspace = None
-    if num_splits > 1:
-        nbytes = _lib.lib().bvllm_decode_workspace_bytes(B, n_heads, num_splits, head_dim)
+    nbytes = _lib.lib().bvllm_decode_workspace_bytes(B, n_heads, n_kv_heads, head_dim, num_splits,
+                                                     blocks_per_split)
+    if nbytes > 0:
         workspace = torch.empty(nbytes // 4, device=q.device, dtype=torch.float32)
     rc = _lib.lib().bvllm_paged_decode(
         q.data_ptr(), q.stride(0), q.stride(1),
@@ -95,7 +93,7 @@ def paged_decode_attention(q, kv_cache, block_tables, seq_lens, scale,
         seq_lens.data_ptr(), float(scale),
         out.data_ptr(), out.stride(0), out.stride(1),
         None if workspace is None else workspace.data_ptr(), num_splits, blocks_per_split,
-        B, n_heads, n_kv_heads, head_dim, block_size, decode_waves(B),
+        B, n_heads, n_kv_heads, head_dim, block_size, decode_waves(),
         _lib.stream_handle(q.device),
     )
     _lib.check(rc, "bvllm_paged_decode")

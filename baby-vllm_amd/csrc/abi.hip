@@ -3,6 +3,8 @@
 #include "bvllm_abi_internal.h"
 #include "bvllm_device.h"
 
+#include <algorithm>
+
 using namespace bvllm;
 
 namespace {
@@ -65,10 +67,17 @@ extern "C" int bvllm_rope_kv_append(void* q, int64_t q_stride_t, int64_t q_strid
   return (int)rope_kv_append(a, (hipStream_t)stream);
 }
 
-extern "C" int64_t bvllm_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_splits,
-                                                int32_t head_dim) {
-  if (num_splits <= 1 || batch <= 0 || num_heads <= 0) return 0;
-  const int64_t rows = (int64_t)batch * num_heads * num_splits;
+extern "C" int64_t bvllm_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                                int32_t head_dim, int32_t num_splits,
+                                                int32_t blocks_per_split) {
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_splits < 1 || blocks_per_split < 1) return 0;
+  DecodeArgs a{};
+  a.batch = batch;
+  a.num_splits = num_splits;
+  a.blocks_per_split = blocks_per_split;
+  const int64_t parts = decode_partials(a);
+  if (parts <= 1) return 0;
+  const int64_t rows = (int64_t)batch * num_heads * parts;
   return rows * head_dim * (int64_t)sizeof(float) + rows * (int64_t)sizeof(float);
 }
 
@@ -101,9 +110,10 @@ extern "C" int bvllm_paged_decode(const void* q, int64_t q_stride_b, int64_t q_s
   if (num_splits < 1 || blocks_per_split < 1) return kBad;
   // Offsets inside one page are 32-bit.
   if ((int64_t)16 * cache_stride_tok > 0x7fffffff) return kBad;
-  if (num_splits > 1 && (!workspace || !aligned16(workspace))) return kBad;
-  if (waves == 0) waves = 8;
-  if (waves != 4 && waves != 8) return kBad;
+  const int64_t ws_bytes = bvllm_decode_workspace_bytes(batch, num_heads, num_kv_heads, head_dim, num_splits,
+                                                        blocks_per_split);
+  if (ws_bytes > 0 && (!workspace || !aligned16(workspace))) return kBad;
+  if (waves != 0 && waves != 4 && waves != 8) return kBad;
 
   DecodeArgs a{};
   a.q = q; a.q_sb = q_stride_b; a.q_sh = q_stride_h;
@@ -114,9 +124,10 @@ extern "C" int bvllm_paged_decode(const void* q, int64_t q_stride_b, int64_t q_s
   a.seq_lens = seq_lens;
   a.scale_log2 = scale * kLog2e;
   a.out = out; a.o_sb = out_stride_b; a.o_sh = out_stride_h;
-  if (num_splits > 1) {
+  if (ws_bytes > 0) {
+    const int64_t rows = ws_bytes / (int64_t)((head_dim + 1) * sizeof(float));
     a.part_out = reinterpret_cast<float*>(workspace);
-    a.part_lse = a.part_out + (int64_t)batch * num_heads * num_splits * head_dim;
+    a.part_lse = a.part_out + rows * head_dim;
   }
   a.num_splits = num_splits; a.blocks_per_split = blocks_per_split;
   a.batch = batch; a.num_heads = num_heads; a.num_kv_heads = num_kv_heads; a.head_dim = head_dim;

@@ -31,11 +31,11 @@ struct DecodeArgs {
   const int32_t* seq_lens;                 // [B]
   float scale_log2;                        // softmax scale · log2(e)
   void* out;      int64_t o_sb, o_sh;      // [B, H, D], written when num_splits == 1
-  float* part_out;                         // [B, H, S, D] fp32, when num_splits > 1
-  float* part_lse;                         // [B, H, S] fp32 (log2 units), when num_splits > 1
+  float* part_out;                         // [B, H, parts, D] fp32 partial outputs
+  float* part_lse;                         // [B, H, parts] fp32 (log2 units)
   int32_t num_splits, blocks_per_split;
   int32_t batch, num_heads, num_kv_heads, head_dim;
-  int32_t waves;                           // waves per work-group (4 or 8)
+  int32_t waves;                           // waves per work-group (4 or 8; 0 = default)
 };
 
 struct PrefillArgs {
@@ -55,6 +55,8 @@ struct PrefillArgs {
 
 hipError_t rope_kv_append(const RopeArgs& a, hipStream_t stream);
 hipError_t paged_decode(const DecodeArgs& a, hipStream_t stream);
+// Partial states (per row and head) one decode launch writes to the workspace.
+int32_t decode_partials(const DecodeArgs& a);
 hipError_t paged_prefill(const PrefillArgs& a, hipStream_t stream);
 
 }  // namespace bvllm

@@ -11,40 +11,76 @@
 // a row that fits in one split gives the same bits whether the launch is the
 // single-pass one (one split) or a split one.
 //
+// Loads: a page of one KV head is 16 token rows of D·2 bytes at a 1 KB stride
+// (7B shape). Both K and V are fetched as 4 whole rows per instruction (lane
+// (n + 16g) reads row 4g+j, bytes 2·(D/16)·n, j < 4), i.e. full 128-byte lines.
+// V is consumed in that layout; K is transposed through a wave-private LDS
+// tile (write in the load layout, read in the MFMA layout, no barrier: a
+// wave's LDS operations complete in order).
+//
 // Per page (16 tokens) and wave, both products run on bf16 MFMA:
 //   Sᵀ[16 tok × 16 col] = K[16 tok × D] · Qᵀ[D × 16 col]   (D/32 × mfma 16x16x32)
 //     col n < G is query head kvh·G + n (the GQA group), the rest is zero padding.
-//     Lane (n + 16g) loads K row n, dims 8(4c+g)..+8 for c < D/32 (16-byte loads);
+//     Lane (n + 16g) reads K row n, dims 8(4c+g)..+8 for c < D/32 from the tile;
 //     the result lane (n + 16g) holds S[head n][token 4g+i], i < 4.
 //   Oᵀ[D × 16 col] += Vᵀ[D × 16 tok] · Pᵀ[16 tok × 16 col]  (D/16 × mfma 16x16x16)
 //     P comes straight from the Sᵀ registers (same lane layout as the B operand);
-//     lane (m + 16g) loads V rows 4g..4g+3, dims (D/16)·m..+D/16 (one 16-byte load
-//     per row at D = 128), and MFMA c takes element c of those rows, so MFMA c's
-//     output row r is dim (D/16)·r + c. Lane (n + 16g) ends up holding
-//     O[head n][dims (D/4)·g .. (D/4)·g + D/4).
+//     MFMA c takes element c of the lane's 4 V rows, so its output row r is dim
+//     (D/16)·r + c. Lane (n + 16g) ends up holding O[head n][dims (D/4)·g .. +D/4).
 // The softmax state (max, sum) of head n lives in lanes n, n+16, n+32, n+48, so
 // the rescale of O by exp(m_old − m_new) needs no cross-lane traffic.
 #include "bvllm_device.h"
 #include "bvllm_abi_internal.h"
 
+#include <stdlib.h>
+
+#include <algorithm>
+
 namespace bvllm {
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+// D/16 bf16 of one row, as a register vector (usable as an asm operand).
+template <int D>
+using RowSlice = typename std::conditional<(D / 16) == 8, u32x4_t, u32x2_t>::type;
 
 template <int D>
 struct PageRegs {
-  uint4 k[D / 32];                      // K row (lane & 15), four 16-byte chunks per lane at D=128
-  typename std::conditional<(D / 16) == 8, uint4, uint2>::type v[4];  // V rows 4g..4g+3
+  RowSlice<D> k[4];  // K rows 4g..4g+3, dims (D/16)·n ..
+  RowSlice<D> v[4];  // V rows 4g..4g+3, dims (D/16)·n ..
 };
+
+// Page loads are issued as inline-asm global loads with explicit waits, so a
+// wave keeps PF pages in flight across its loop: the compiler's own waitcnt
+// insertion drains every outstanding load at a loop header, which would
+// serialise memory latency and compute. wait_page<N>() waits until at most N
+// loads are outstanding and is tied to the page's registers, so no use of
+// them can move above it. Every asm load is followed, before its registers go
+// dead, by a wait that covers it (the loop's drain).
+template <int D>
+__device__ __forceinline__ void gload(RowSlice<D>& r, const uint16_t* base, uint32_t off_elems) {
+  const uint32_t off = off_elems * 2;
+  if constexpr (D / 16 == 8) asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(r) : "v"(off), "s"(base));
+  else asm volatile("global_load_dwordx2 %0, %1, %2" : "=v"(r) : "v"(off), "s"(base));
+}
 
 template <int D>
 __device__ __forceinline__ void load_page(PageRegs<D>& r, const uint16_t* kbase, const uint16_t* vbase,
-                                          const uint32_t (&koff)[D / 32], const uint32_t (&voff)[4]) {
+                                          const uint32_t (&off)[4]) {
 #pragma unroll
-  for (int c = 0; c < D / 32; ++c) r.k[c] = ld16(kbase + koff[c]);
+  for (int j = 0; j < 4; ++j) gload<D>(r.k[j], kbase, off[j]);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if constexpr (D / 16 == 8) r.v[j] = ld16(vbase + voff[j]);
-    else r.v[j] = ld8(vbase + voff[j]);
-  }
+  for (int j = 0; j < 4; ++j) gload<D>(r.v[j], vbase, off[j]);
+}
+
+constexpr int kLoadsPerPage = 8;
+
+template <int N, int D>
+__device__ __forceinline__ void wait_page(PageRegs<D>& r) {
+  asm volatile("s_waitcnt vmcnt(%8)"
+               : "+v"(r.k[0]), "+v"(r.k[1]), "+v"(r.k[2]), "+v"(r.k[3]),
+                 "+v"(r.v[0]), "+v"(r.v[1]), "+v"(r.v[2]), "+v"(r.v[3])
+               : "n"(N));
 }
 
 template <int D>
@@ -54,37 +90,36 @@ struct WaveState {
   f32x4_t acc[D / 16];  // acc[c][i] = O[head][(D/16)·(4g+i) + c]
 };
 
+// One page of the online softmax. Tokens at or past tok_limit are masked: their
+// scores become -inf and their V rows are replaced by zeros where they are used
+// (unwritten slots may hold NaN, and 0·NaN would poison the PV product). The
+// masking is branch-free so that the loads of the pages in flight stay in flight.
 template <int D>
-__device__ __forceinline__ void process_page(WaveState<D>& st, PageRegs<D>& r, const uint4 (&qb)[D / 32],
-                                             int page, int seq_len, float scale_log2, int g) {
+__device__ __forceinline__ void process_page(WaveState<D>& st, const PageRegs<D>& r, const uint4 (&qb)[D / 32],
+                                             unsigned char* tile, int n, int g,
+                                             int tok0, int tok_limit, float scale_log2) {
   constexpr int VD = D / 16;
+  constexpr int PITCH = 2 * D + 16;  // bytes; the pad keeps 16-row column reads conflict-free
+#pragma unroll
+  for (int j = 0; j < 4; ++j) *reinterpret_cast<RowSlice<D>*>(tile + (4 * g + j) * PITCH + 2 * VD * n) = r.k[j];
+  asm volatile("" ::: "memory");
   f32x4_t s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int c = 0; c < D / 32; ++c) s = mfma_16x16x32(r.k[c], qb[c], s);
+  for (int c = 0; c < D / 32; ++c) s = mfma_16x16x32(ld16(tile + n * PITCH + 16 * (4 * c + g)), qb[c], s);
+  asm volatile("" ::: "memory");
 
-  const int tok0 = page * 16 + 4 * g;
-  const bool partial = page * 16 + 16 > seq_len;  // wave-uniform
+  bool live[4];
   float sv[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) sv[i] = s[i] * scale_log2;
-  if (partial) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (tok0 + i >= seq_len) sv[i] = kNegInf;
-    }
-    // Slots past seq_len may never have been written (NaN); P is 0 there, and
-    // 0·NaN would poison the PV product, so the rows are zeroed.
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (tok0 + j >= seq_len) {
-        if constexpr (VD == 8) r.v[j] = make_uint4(0, 0, 0, 0);
-        else r.v[j] = make_uint2(0, 0);
-      }
-    }
+  for (int i = 0; i < 4; ++i) {
+    live[i] = tok0 + i < tok_limit;
+    sv[i] = live[i] ? s[i] * scale_log2 : kNegInf;
   }
   float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
   mx = max_across_groups(mx);
   const float m_new = fmaxf(st.m, mx);
+  // A page with no live token leaves the state bit-identical: m_new == m,
+  // alpha == 1 and p == 0 (the wave's first page always has a live token).
   const float alpha = fast_exp2(st.m - m_new);
   float p[4];
 #pragma unroll
@@ -97,29 +132,27 @@ __device__ __forceinline__ void process_page(WaveState<D>& st, PageRegs<D>& r, c
   uint2 pb;
   pb.x = pack_bf16x2(p[0], p[1]);
   pb.y = pack_bf16x2(p[2], p[3]);
+  constexpr int VW = VD / 2;  // dwords per V row slice
+  uint32_t vv[4][VW];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int x = 0; x < VW; ++x) vv[j][x] = live[j] ? r.v[j][x] : 0u;
+  }
 #pragma unroll
   for (int c = 0; c < VD; ++c) {
     uint2 va;
-    if constexpr (VD == 8) {
-      const uint32_t* v0 = reinterpret_cast<const uint32_t*>(&r.v[0]);
-      const uint32_t* v1 = reinterpret_cast<const uint32_t*>(&r.v[1]);
-      const uint32_t* v2 = reinterpret_cast<const uint32_t*>(&r.v[2]);
-      const uint32_t* v3 = reinterpret_cast<const uint32_t*>(&r.v[3]);
-      va.x = pick_halves(v0[c / 2], v1[c / 2], c & 1);
-      va.y = pick_halves(v2[c / 2], v3[c / 2], c & 1);
-    } else {
-      const uint32_t* v0 = reinterpret_cast<const uint32_t*>(&r.v[0]);
-      const uint32_t* v1 = reinterpret_cast<const uint32_t*>(&r.v[1]);
-      const uint32_t* v2 = reinterpret_cast<const uint32_t*>(&r.v[2]);
-      const uint32_t* v3 = reinterpret_cast<const uint32_t*>(&r.v[3]);
-      va.x = pick_halves(v0[c / 2], v1[c / 2], c & 1);
-      va.y = pick_halves(v2[c / 2], v3[c / 2], c & 1);
-    }
+    va.x = pick_halves(vv[0][c / 2], vv[1][c / 2], c & 1);
+    va.y = pick_halves(vv[2][c / 2], vv[3][c / 2], c & 1);
     st.acc[c] = mfma_16x16x16(va, pb, st.acc[c]);
   }
 }
 
-template <int D, int NW>
+// Bytes of one wave's K transpose tile: 16 rows of D bf16 + 16 bytes of pad.
+template <int D>
+constexpr int kTileBytes = 16 * (2 * D + 16);
+
+template <int D, int NW, int PF>
 __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
   constexpr int KC = D / 32;
   constexpr int VD = D / 16;
@@ -159,11 +192,11 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
   for (int c = 0; c < VD; ++c) st.acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  uint32_t koff[KC], voff[4];
+  uint32_t off[4];
 #pragma unroll
-  for (int c = 0; c < KC; ++c) koff[c] = (uint32_t)(n * a.c_st + 8 * (4 * c + g));
-#pragma unroll
-  for (int j = 0; j < 4; ++j) voff[j] = (uint32_t)((4 * g + j) * a.c_st + VD * n);
+  for (int j = 0; j < 4; ++j) off[j] = (uint32_t)((4 * g + j) * a.c_st + VD * n);
+  // This wave's K transpose tile, then the per-wave merge records.
+  unsigned char* tile = reinterpret_cast<unsigned char*>(smem) + w * kTileBytes<D>;
 
   const uint16_t* kc = reinterpret_cast<const uint16_t*>(a.k_cache) + (int64_t)kvh * a.c_sh;
   const uint16_t* vc = reinterpret_cast<const uint16_t*>(a.v_cache) + (int64_t)kvh * a.c_sh;
@@ -171,40 +204,54 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
 
   const int first = start + w;
   const int cnt = (end > first) ? (end - first + NW - 1) / NW : 0;
+  // Lane k holds the table entry of this wave's page number base + k. The first
+  // slice is requested together with seq_len and q (its index is clamped into
+  // the row, so it does not wait for seq_len); entries past the row are unused.
+  int ent = bt[min(first + NW * lane, a.max_blocks - 1)];
   for (int base = 0; base < cnt; base += 64) {
     const int here = min(64, cnt - base);
-    // Lane k holds the table entry of this wave's page number base + k.
-    int ent = 0;
-    if (lane < here) ent = bt[first + NW * (base + lane)];
-    ent = min(max(ent, 0), a.num_pages - 1);
-    auto phys = [&](int k) -> int64_t { return (int64_t)__builtin_amdgcn_readlane(ent, k); };
+    if (base > 0) ent = bt[min(first + NW * (base + lane), a.max_blocks - 1)];
+    const int slot_ent = min(max(ent, 0), a.num_pages - 1);
+    auto phys = [&](int k) -> int64_t { return (int64_t)__builtin_amdgcn_readlane(slot_ent, k); };
 
-    PageRegs<D> r0, r1;
-    {
-      const int64_t p0 = phys(0) * a.c_sb;
-      load_page<D>(r0, kc + p0, vc + p0, koff, voff);
-      const int64_t p1 = phys(min(1, here - 1)) * a.c_sb;
-      load_page<D>(r1, kc + p1, vc + p1, koff, voff);
+    // PF pages in flight per wave: page k+PF is requested as soon as page k is
+    // consumed. Loads are issued unconditionally (page index clamped into the
+    // wave's range) and the page count is padded to a multiple of PF with fully
+    // masked pages, so every wait counts exactly PF-1 younger pages.
+    PageRegs<D> r[PF];
+    const uint16_t* kpage[PF];
+    const uint16_t* vpage[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int64_t p = phys(min(i, here - 1)) * a.c_sb;
+      load_page<D>(r[i], kc + p, vc + p, off);
     }
-    for (int k = 0; k < here; k += 2) {
-      process_page<D>(st, r0, qb, first + NW * (base + k), seq_len, a.scale_log2, g);
-      {
-        const int64_t pn = phys(min(k + 2, here - 1)) * a.c_sb;
-        load_page<D>(r0, kc + pn, vc + pn, koff, voff);
-      }
-      if (k + 1 < here) {
-        process_page<D>(st, r1, qb, first + NW * (base + k + 1), seq_len, a.scale_log2, g);
-        const int64_t pn = phys(min(k + 3, here - 1)) * a.c_sb;
-        load_page<D>(r1, kc + pn, vc + pn, koff, voff);
+    (void)kpage;
+    (void)vpage;
+    const int padded = (here + PF - 1) / PF * PF;
+    for (int k = 0; k < padded; k += PF) {
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        wait_page<(PF - 1) * kLoadsPerPage, D>(r[i]);
+        const int page = first + NW * (base + k + i);
+        const int limit = (k + i < here) ? seq_len : 0;
+        process_page<D>(st, r[i], qb, tile, n, g, page * 16 + 4 * g, limit, a.scale_log2);
+        const int64_t pn = phys(min(k + i + PF, here - 1)) * a.c_sb;
+        load_page<D>(r[i], kc + pn, vc + pn, off);
       }
     }
+    // Drain: the loads issued for pages past the end must land before their
+    // registers are reused.
+#pragma unroll
+    for (int i = 0; i < PF; ++i) wait_page<0, D>(r[i]);
   }
   const float l_tot = sum_across_groups(st.l);
 
   // Merge the NW wave states in wave order. LDS layout per wave:
   //   m[16], l[16], acc[G][D].
   const int wstride = 32 + G * D;
-  float* my = smem + w * wstride;
+  float* merge = smem + NW * kTileBytes<D> / 4;
+  float* my = merge + w * wstride;
   if (g == 0) {
     my[n] = st.m;
     my[16 + n] = l_tot;
@@ -225,13 +272,13 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
     const int d = (e * 4) % D;
     float M = kNegInf;
 #pragma unroll
-    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, smem[ww * wstride + h]);
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, merge[ww * wstride + h]);
     float L = 0.f;
     float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
     if (M != kNegInf) {
 #pragma unroll
       for (int ww = 0; ww < NW; ++ww) {
-        const float* ws = smem + ww * wstride;
+        const float* ws = merge + ww * wstride;
         const float wgt = fast_exp2(ws[h] - M);
         L += ws[16 + h] * wgt;
         const float4 x = *reinterpret_cast<const float4*>(ws + 32 + h * D + d);
@@ -259,22 +306,26 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
   }
 }
 
-// One work-group per (sequence, query head): out = Σ_s w_s·o_s / Σ_s w_s with
-// w_s = 2^(lse_s − max lse). Thread (chunk, group) accumulates splits
-// group, group + NG, ... in order, then the NG group sums are added in group
-// order, so trailing empty splits (w = 0, o = 0) leave the bits unchanged.
+// One work-group per (sequence, query head, 32-dim slice):
+//   out = Σ_s w_s·o_s / Σ_s w_s,  w_s = 2^(lse_s − max lse).
+// Thread (chunk, group) accumulates splits group, group + 32, ... in order, then
+// the 32 group sums are added in group order. The grouping depends only on the
+// split index, so trailing empty splits (w = 0, o = 0) leave the bits unchanged.
 template <int D>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeArgs a) {
-  constexpr int CH = D / 4;       // float4 chunks per row
+  constexpr int DS = 32;          // dims per work-group
+  constexpr int CH = DS / 4;      // float4 chunks per slice
   constexpr int NG = 256 / CH;    // split groups
+  constexpr int SLICES = D / DS;
   __shared__ float red[256];
   __shared__ float4 gnum[NG][CH];
   __shared__ float gden[NG];
 
-  const int bh = blockIdx.x;
+  const int bh = blockIdx.x / SLICES;
+  const int d0 = (blockIdx.x % SLICES) * DS;
   const int S = a.num_splits;
   const float* lse = a.part_lse + (int64_t)bh * S;
-  const float* po = a.part_out + (int64_t)bh * S * D;
+  const float* po = a.part_out + (int64_t)bh * S * D + d0;
 
   float M = kNegInf;
   for (int s = threadIdx.x; s < S; s += 256) M = fmaxf(M, lse[s]);
@@ -291,6 +342,7 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeArgs a) {
   const int grp = threadIdx.x / CH;
   float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
   float den = 0.f;
+#pragma unroll 4
   for (int s = grp; s < S; s += NG) {
     const float wgt = fast_exp2(lse[s] - M);
     const float4 x = *reinterpret_cast<const float4*>(po + (int64_t)s * D + 4 * ch);
@@ -317,7 +369,7 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeArgs a) {
     const float inv = 1.f / (dd == 0.f ? 1.f : dd);
     const int b = bh / a.num_heads;
     const int h = bh % a.num_heads;
-    uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + 4 * ch;
+    uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d0 + 4 * ch;
     uint2 pk;
     pk.x = pack_bf16x2(t.x * inv, t.y * inv);
     pk.y = pack_bf16x2(t.z * inv, t.w * inv);
@@ -325,34 +377,118 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeArgs a) {
   }
 }
 
-template <int D, int NW>
+// Reduce for at most 32 partial states per (row, head): one thread per
+// (row, head, 4 dims) accumulates the partials in order. With ≤ 32 partials
+// every group of decode_reduce_kernel holds at most one non-empty partial, so
+// both kernels return the same bits for the same row (trailing empty partials
+// add exact zeros in either).
+template <int D>
+__global__ __launch_bounds__(256) void decode_reduce_small_kernel(DecodeArgs a, int64_t items) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= items) return;
+  const int64_t bh = t / (D / 4);
+  const int d = (int)(t - bh * (D / 4)) * 4;
+  const int S = a.num_splits;
+  const float* lse = a.part_lse + bh * S;
+  const float* po = a.part_out + bh * S * D + d;
+  float M = kNegInf;
+#pragma unroll 8
+  for (int s = 0; s < S; ++s) M = fmaxf(M, lse[s]);
+  if (M == kNegInf) M = 0.f;
+  float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
+  float den = 0.f;
+#pragma unroll 8
+  for (int s = 0; s < S; ++s) {
+    const float wgt = fast_exp2(lse[s] - M);
+    const float4 x = *reinterpret_cast<const float4*>(po + (int64_t)s * D);
+    num.x += wgt * x.x;
+    num.y += wgt * x.y;
+    num.z += wgt * x.z;
+    num.w += wgt * x.w;
+    den += wgt;
+  }
+  const float inv = 1.f / (den == 0.f ? 1.f : den);
+  const int b = (int)(bh / a.num_heads);
+  const int h = (int)(bh % a.num_heads);
+  uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d;
+  uint2 pk;
+  pk.x = pack_bf16x2(num.x * inv, num.y * inv);
+  pk.y = pack_bf16x2(num.z * inv, num.w * inv);
+  st8(dst, pk);
+}
+
+template <int D>
+static hipError_t launch_reduce(const DecodeArgs& r, hipStream_t stream) {
+  if (r.num_splits <= 32) {
+    const int64_t items = (int64_t)r.batch * r.num_heads * (D / 4);
+    hipLaunchKernelGGL((decode_reduce_small_kernel<D>), dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
+                       stream, r, items);
+  } else {
+    hipLaunchKernelGGL((decode_reduce_kernel<D>), dim3((unsigned)(r.batch * r.num_heads * (D / 32))), dim3(256),
+                       0, stream, r);
+  }
+  return hipGetLastError();
+}
+
+template <int D, int NW, int PF>
 static hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
   const int G = a.num_heads / a.num_kv_heads;
-  const size_t smem = (size_t)NW * (32 + G * D) * sizeof(float);
+  const size_t smem = (size_t)NW * kTileBytes<D> + (size_t)NW * (32 + G * D) * sizeof(float);
+  if (smem > 160 * 1024) return hipErrorInvalidValue;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_decode_kernel<D, NW, PF>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
   const int64_t wgs = (int64_t)a.batch * a.num_kv_heads * a.num_splits;
   if (wgs == 0) return hipSuccess;
   if (wgs > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((paged_decode_kernel<D, NW>), dim3((unsigned)wgs), dim3(NW * 64), smem, stream, a);
+  hipLaunchKernelGGL((paged_decode_kernel<D, NW, PF>), dim3((unsigned)wgs), dim3(NW * 64), smem, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || a.num_splits == 1) return err;
-  hipLaunchKernelGGL((decode_reduce_kernel<D>), dim3((unsigned)(a.batch * a.num_heads)), dim3(256), 0,
-                     stream, a);
-  return hipGetLastError();
+  return launch_reduce<D>(a, stream);
+}
+
+// Pages in flight per wave; BVLLM_DECODE_DEPTH (2, 3 or 4) overrides the default for tuning.
+// Two is best measured on MI355X: deeper queues lose DRAM efficiency on the
+// 256-byte head slices.
+static int decode_depth() {
+  static const int depth = [] {
+    const char* e = getenv("BVLLM_DECODE_DEPTH");
+    const int v = e ? atoi(e) : 0;
+    return (v >= 2 && v <= 4) ? v : 2;
+  }();
+  return depth;
+}
+
+template <int D, int NW>
+static hipError_t decode_for_depth(const DecodeArgs& a, hipStream_t stream) {
+  switch (decode_depth()) {
+    case 2: return launch_decode<D, NW, 2>(a, stream);
+    case 4: return launch_decode<D, NW, 4>(a, stream);
+    default: return launch_decode<D, NW, 3>(a, stream);
+  }
 }
 
 template <int D>
 static hipError_t decode_for_dim(const DecodeArgs& a, hipStream_t stream) {
   switch (a.waves) {
-    case 4: return launch_decode<D, 4>(a, stream);
-    case 8: return launch_decode<D, 8>(a, stream);
+    case 4: return decode_for_depth<D, 4>(a, stream);
+    case 8: return decode_for_depth<D, 8>(a, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
+int32_t decode_partials(const DecodeArgs& a) { return a.num_splits; }
+
 hipError_t paged_decode(const DecodeArgs& a, hipStream_t stream) {
+  DecodeArgs d = a;
+  if (d.waves == 0) d.waves = 4;
   switch (a.head_dim) {
-    case 64: return decode_for_dim<64>(a, stream);
-    case 128: return decode_for_dim<128>(a, stream);
+    case 64: return decode_for_dim<64>(d, stream);
+    case 128: return decode_for_dim<128>(d, stream);
     default: return hipErrorInvalidValue;
   }
 }

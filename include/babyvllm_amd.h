@@ -37,7 +37,7 @@ extern "C" {
 #endif
 
 /* ABI version of this header; bumped on any signature change. */
-#define BVLLM_ABI_VERSION 1
+#define BVLLM_ABI_VERSION 2
 
 #if defined(__GNUC__)
 #define BVLLM_API __attribute__((visibility("default")))
@@ -74,12 +74,13 @@ BVLLM_API int bvllm_rope_kv_append(void* q, int64_t q_stride_t, int64_t q_stride
                          int32_t head_dim, void* stream);
 
 /*
- * Bytes of fp32 scratch bvllm_paged_decode needs for a split launch:
- * part_out [B, H, S, D] followed by part_lse [B, H, S] (the reference's
- * part_out / part_lse, babyvllm/kernels/paged_attn.py:317-318). 0 when num_splits <= 1.
+ * Bytes of device scratch bvllm_paged_decode needs for one launch (0 = none):
+ * fp32 partial outputs [B, H, S, D] and log-sum-exps [B, H, S] of every split,
+ * the reference's part_out / part_lse (babyvllm/kernels/paged_attn.py:317-318).
  */
-BVLLM_API int64_t bvllm_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_splits,
-                                     int32_t head_dim);
+BVLLM_API int64_t bvllm_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                               int32_t head_dim, int32_t num_splits,
+                                               int32_t blocks_per_split);
 
 /*
  * Paged decode attention, one query token per sequence. Replaces
@@ -92,9 +93,9 @@ BVLLM_API int64_t bvllm_decode_workspace_bytes(int32_t batch, int32_t num_heads,
  * (num_splits, blocks_per_split) is the flash-decoding plan
  * (decode_split_plan, babyvllm/kernels/decode_split.py:48-79): split s covers
  * pages [s·bps, (s+1)·bps), the last split runs to the row's last page.
- * num_splits > 1 needs `workspace` of bvllm_decode_workspace_bytes() bytes.
- * `waves` (0 = choose) is the number of 64-lane waves per work-group; it must
- * be the same for launches whose bits are compared.
+ * `workspace` must hold bvllm_decode_workspace_bytes() bytes when that is > 0.
+ * `waves` is the number of 64-lane waves per work-group: 0 (the library's
+ * choice), 4 or 8; launches whose bits are compared must use the same value.
  */
 BVLLM_API int bvllm_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                        const void* k_cache, const void* v_cache,

@@ -64,8 +64,10 @@ def test_abi_version_matches_header():
 
 def test_workspace_bytes_formula():
     h = _lib().lib()
-    assert h.bvllm_decode_workspace_bytes(8, 28, 15, 128) == 8 * 28 * 15 * (128 + 1) * 4
-    assert h.bvllm_decode_workspace_bytes(64, 28, 1, 128) == 0
+    # B8: 15 splits -> 15 partial states per (row, head).
+    assert h.bvllm_decode_workspace_bytes(8, 28, 4, 128, 15, 8) == 8 * 28 * 15 * (128 + 1) * 4
+    # Single pass: no scratch.
+    assert h.bvllm_decode_workspace_bytes(64, 28, 4, 128, 1, 120) == 0
 
 
 def test_host_side_argument_rejection():
@@ -84,6 +86,9 @@ def test_host_side_argument_rejection():
     assert h.bvllm_paged_decode(None, 0, 0, None, None, 0, 0, 0, 0, None, 0, 0, None, 1.0,
                                 None, 0, 0, None, 1, 1, 1, 34, 2, 128, 16, 0, None) == bad
     assert b"invalid argument" in h.bvllm_error_string(bad)
+    # waves must be 0, 4 or 8
+    assert h.bvllm_paged_decode(None, 0, 0, None, None, 0, 0, 0, 0, None, 0, 0, None, 1.0,
+                                None, 0, 0, None, 1, 1, 1, 28, 4, 128, 16, 5, None) == bad
     # Nothing to do is a success that launches nothing.
     assert h.bvllm_paged_decode(None, 0, 0, None, None, 0, 0, 0, 0, None, 0, 0, None, 1.0,
                                 None, 0, 0, None, 1, 1, 0, 28, 4, 128, 16, 0, None) == 0
