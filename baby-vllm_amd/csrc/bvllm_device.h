@@ -32,9 +32,23 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
   return u >> 16;
 }
 
-// Two floats -> one dword of packed bf16 (lo in bits 0..15), RNE.
+// Two floats -> one dword of packed bf16 (lo in bits 0..15), RNE, NaN -> 0x7fc0.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return f32_to_bf16_rne(lo) | (f32_to_bf16_rne(hi) << 16);
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16 with the hardware converter (v_cvt_pk_bf16_f32,
+// round to nearest even). Same bits as pack_bf16x2 for every non-NaN input.
+__device__ __forceinline__ uint32_t pack_bf16x2_hw(float lo, float hi) {
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// True when every active lane of the wave holds x == 1.
+__device__ __forceinline__ bool wave_all_one(float x) {
+  return __builtin_amdgcn_ballot_w64(x != 1.f) == 0;
 }
 
 // Low / high bf16 of a dword as float.

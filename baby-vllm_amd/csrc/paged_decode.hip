@@ -126,12 +126,14 @@ __device__ __forceinline__ void process_page(WaveState<D>& st, const PageRegs<D>
   for (int i = 0; i < 4; ++i) p[i] = fast_exp2(sv[i] - m_new);
   st.l = st.l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
   st.m = m_new;
+  if (!wave_all_one(alpha)) {  // x·1 == x: skipping is exact
 #pragma unroll
-  for (int c = 0; c < VD; ++c) st.acc[c] *= alpha;
+    for (int c = 0; c < VD; ++c) st.acc[c] *= alpha;
+  }
 
   uint2 pb;
-  pb.x = pack_bf16x2(p[0], p[1]);
-  pb.y = pack_bf16x2(p[2], p[3]);
+  pb.x = pack_bf16x2_hw(p[0], p[1]);
+  pb.y = pack_bf16x2_hw(p[2], p[3]);
   constexpr int VW = VD / 2;  // dwords per V row slice
   uint32_t vv[4][VW];
 #pragma unroll
@@ -295,8 +297,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
     if (a.num_splits == 1) {
       uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)b * a.o_sb + (int64_t)head * a.o_sh + d;
       uint2 pk;
-      pk.x = pack_bf16x2(o.x, o.y);
-      pk.y = pack_bf16x2(o.z, o.w);
+      pk.x = pack_bf16x2_hw(o.x, o.y);
+      pk.y = pack_bf16x2_hw(o.z, o.w);
       st8(dst, pk);
     } else {
       const int64_t row = ((int64_t)b * a.num_heads + head) * a.num_splits + split;
@@ -371,8 +373,8 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeArgs a) {
     const int h = bh % a.num_heads;
     uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d0 + 4 * ch;
     uint2 pk;
-    pk.x = pack_bf16x2(t.x * inv, t.y * inv);
-    pk.y = pack_bf16x2(t.z * inv, t.w * inv);
+    pk.x = pack_bf16x2_hw(t.x * inv, t.y * inv);
+    pk.y = pack_bf16x2_hw(t.z * inv, t.w * inv);
     st8(dst, pk);
   }
 }
@@ -412,8 +414,8 @@ __global__ __launch_bounds__(256) void decode_reduce_small_kernel(DecodeArgs a, 
   const int h = (int)(bh % a.num_heads);
   uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d;
   uint2 pk;
-  pk.x = pack_bf16x2(num.x * inv, num.y * inv);
-  pk.y = pack_bf16x2(num.z * inv, num.w * inv);
+  pk.x = pack_bf16x2_hw(num.x * inv, num.y * inv);
+  pk.y = pack_bf16x2_hw(num.z * inv, num.w * inv);
   st8(dst, pk);
 }
 

@@ -22,7 +22,7 @@
 namespace bvllm {
 
 template <int D, int NW, int QT>
-__global__ __launch_bounds__(NW * 64) void paged_prefill_kernel(PrefillArgs a, int n_qb, int total_wg,
+__global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a, int n_qb, int total_wg,
                                                                   int per_xcd) {
   constexpr int KT = 64;
   constexpr int PITCH = D + 8;  // bf16 elements; 16-byte pad keeps 16-row column reads conflict-free
@@ -200,14 +200,16 @@ __global__ __launch_bounds__(NW * 64) void paged_prefill_kernel(PrefillArgs a, i
           }
         l[ct] = l[ct] * alpha + psum;
         m[ct] = m_new;
+        if (!wave_all_one(alpha)) {  // x·1 == x: skipping is exact
 #pragma unroll
-        for (int c = 0; c < VD; ++c) acc[ct][c] *= alpha;
+          for (int c = 0; c < VD; ++c) acc[ct][c] *= alpha;
+        }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          pb[ct][u].x = pack_bf16x2(p[2 * u][0], p[2 * u][1]);
-          pb[ct][u].y = pack_bf16x2(p[2 * u][2], p[2 * u][3]);
-          pb[ct][u].z = pack_bf16x2(p[2 * u + 1][0], p[2 * u + 1][1]);
-          pb[ct][u].w = pack_bf16x2(p[2 * u + 1][2], p[2 * u + 1][3]);
+          pb[ct][u].x = pack_bf16x2_hw(p[2 * u][0], p[2 * u][1]);
+          pb[ct][u].y = pack_bf16x2_hw(p[2 * u][2], p[2 * u][3]);
+          pb[ct][u].z = pack_bf16x2_hw(p[2 * u + 1][0], p[2 * u + 1][1]);
+          pb[ct][u].w = pack_bf16x2_hw(p[2 * u + 1][2], p[2 * u + 1][3]);
         }
       }
 
@@ -251,15 +253,15 @@ __global__ __launch_bounds__(NW * 64) void paged_prefill_kernel(PrefillArgs a, i
     for (int i = 0; i < 4; ++i) {
       if constexpr (VD == 8) {
         uint4 pk;
-        pk.x = pack_bf16x2(acc[ct][0][i] * inv, acc[ct][1][i] * inv);
-        pk.y = pack_bf16x2(acc[ct][2][i] * inv, acc[ct][3][i] * inv);
-        pk.z = pack_bf16x2(acc[ct][4][i] * inv, acc[ct][5][i] * inv);
-        pk.w = pack_bf16x2(acc[ct][6][i] * inv, acc[ct][7][i] * inv);
+        pk.x = pack_bf16x2_hw(acc[ct][0][i] * inv, acc[ct][1][i] * inv);
+        pk.y = pack_bf16x2_hw(acc[ct][2][i] * inv, acc[ct][3][i] * inv);
+        pk.z = pack_bf16x2_hw(acc[ct][4][i] * inv, acc[ct][5][i] * inv);
+        pk.w = pack_bf16x2_hw(acc[ct][6][i] * inv, acc[ct][7][i] * inv);
         st16(orow + VD * i, pk);
       } else {
         uint2 pk;
-        pk.x = pack_bf16x2(acc[ct][0][i] * inv, acc[ct][1][i] * inv);
-        pk.y = pack_bf16x2(acc[ct][2][i] * inv, acc[ct][3][i] * inv);
+        pk.x = pack_bf16x2_hw(acc[ct][0][i] * inv, acc[ct][1][i] * inv);
+        pk.y = pack_bf16x2_hw(acc[ct][2][i] * inv, acc[ct][3][i] * inv);
         st8(orow + VD * i, pk);
       }
     }

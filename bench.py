@@ -301,7 +301,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary lines")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default=None, help="decode_b64 | decode_b8 | decode_b1 | append | prefill")
+    ap.add_argument("--only", default=None,
+                    help="decode_b64 | decode_b8 | decode_b1 | append | prefill | prefill:<shape>")
     ap.add_argument("--calib-copy", action="store_true")
     args = ap.parse_args()
 
@@ -337,6 +338,10 @@ def main():
     if args.only == "prefill":
         print(json.dumps({n: bench_prefill(n, args.warmup, args.steps) for n in PREFILL_SHAPES}),
               flush=True)
+        return
+    if args.only and args.only.startswith("prefill:"):
+        name = args.only.split(":", 1)[1]
+        print(json.dumps({name: bench_prefill(name, args.warmup, args.steps)}), flush=True)
         return
 
     log("headline: decode B64 ctx1920 ...")
