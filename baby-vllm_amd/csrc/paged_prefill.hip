@@ -33,6 +33,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   constexpr int CHUNKS = KT * CPR;
   constexpr int PER_T = CHUNKS / (NW * 64);
   static_assert(PER_T * NW * 64 == CHUNKS, "tile chunks must divide evenly over the work-group");
+  static_assert(KT == 64, "a key tile spans four 16-token pages");
   typedef typename std::conditional<VD == 8, uint4, uint2>::type VRow;
 
   __shared__ __attribute__((aligned(16))) uint16_t lds_k[2][KT * PITCH];
@@ -89,6 +90,14 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
       qreg[ct][c] = valid[ct] ? ld16(qrow + 8 * (4 * c + g)) : make_uint4(0, 0, 0, 0);
   }
 
+  // Make the Q loads complete here, once: otherwise they look pending at the
+  // key loop's header and the compiler drains every load there, including the
+  // next tile's staging loads, on each iteration.
+#pragma unroll
+  for (int ct = 0; ct < QT; ++ct)
+#pragma unroll
+    for (int c = 0; c < KC; ++c) asm volatile("" ::"v"(qreg[ct][c].x), "v"(qreg[ct][c].y), "v"(qreg[ct][c].z), "v"(qreg[ct][c].w));
+
   float m[QT], l[QT];
   f32x4_t acc[QT][VD];
 #pragma unroll
@@ -103,8 +112,25 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   const uint16_t* vc = reinterpret_cast<const uint16_t*>(a.v_cache) + (int64_t)kvh * a.c_sh;
   const int32_t* bt = a.block_tables + (int64_t)s * a.bt_stride;
 
+  // The four page numbers of a key tile are fetched first, as scalar loads
+  // (constant address space, counted apart from the vector loads), and then all
+  // data loads of the tile are issued back to back.
+  typedef const int32_t __attribute__((address_space(4)))* ConstI32;
+  const ConstI32 bts = (ConstI32)bt;
+  constexpr int PAGES_PER_TILE = KT / 16;
   uint4 stk[PER_T], stv[PER_T];
   auto stage_load = [&](int kt) {
+    int64_t page_off[PAGES_PER_TILE];
+#pragma unroll
+    for (int pg = 0; pg < PAGES_PER_TILE; ++pg) {
+      int phys = bts[min(kt * PAGES_PER_TILE + pg, a.max_blocks - 1)];
+      phys = min(max(phys, 0), a.num_pages - 1);
+      page_off[pg] = (int64_t)phys * a.c_sb;
+    }
+    // Keep the four table loads together ahead of the data loads (the compiler
+    // would otherwise sink each into the branch that uses it, one wait apiece).
+#pragma unroll
+    for (int pg = 0; pg < PAGES_PER_TILE; ++pg) asm volatile("" ::"s"(page_off[pg]));
 #pragma unroll
     for (int r = 0; r < PER_T; ++r) {
       const int e = threadIdx.x + r * NW * 64;
@@ -112,9 +138,9 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
       const int part = e - key * CPR;
       const int pos = kt * KT + key;
       if (pos < hi) {
-        int phys = bt[min(pos >> 4, a.max_blocks - 1)];
-        phys = min(max(phys, 0), a.num_pages - 1);
-        const int64_t off = (int64_t)phys * a.c_sb + (int64_t)(pos & 15) * a.c_st + part * 8;
+        const int pg = key >> 4;  // selects instead of a dynamically indexed private array
+        const int64_t po = pg == 0 ? page_off[0] : pg == 1 ? page_off[1] : pg == 2 ? page_off[2] : page_off[3];
+        const int64_t off = po + (int64_t)(pos & 15) * a.c_st + part * 8;
         stk[r] = ld16(kc + off);
         stv[r] = ld16(vc + off);
       } else {
@@ -140,9 +166,13 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   }
   __syncthreads();
 
+  // Staging runs on every iteration, also the last: tile n_tiles lies wholly at
+  // or past hi, so it issues no data load and stores zeros into the idle
+  // buffer. Branching on kt + 1 < n_tiles instead would leave the loads looking
+  // pending at the loop header, and the compiler would drain them there.
   for (int kt = 0; kt < n_tiles; ++kt) {
     const int buf = kt & 1;
-    if (kt + 1 < n_tiles) stage_load(kt + 1);
+    stage_load(kt + 1);
 
     if (wave_live && kt * KT <= wave_hi) {
       const uint16_t* K = lds_k[buf];
@@ -238,7 +268,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
       }
     }
 
-    if (kt + 1 < n_tiles) stage_store(buf ^ 1);
+    stage_store(buf ^ 1);
     __syncthreads();
   }
 
