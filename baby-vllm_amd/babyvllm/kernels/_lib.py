@@ -56,12 +56,13 @@ SIGNATURES = {
         _p, _p, _p, _f32,           # query_start_loc, seq_lens, context_lens, scale
         _p, _i64, _i64,             # out
         _i32, _i32, _i32,           # num_seqs, num_tokens, max_query_len
+        _i32,                       # single_query_seqs (-1 = unknown)
         _i32, _i32, _i32, _i32,     # H, Hkv, D, block_size
         _p,                         # stream
     ]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class KernelLibraryError(RuntimeError):

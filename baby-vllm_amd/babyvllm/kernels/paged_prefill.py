@@ -14,6 +14,18 @@ import torch
 from babyvllm.kernels import _lib
 
 
+def _single_query_seqs(md, num_seqs):
+    """Sequences with exactly one query token, from the host copy of query_start_loc.
+
+    -1 (unknown) when the metadata carries no host copy of the right length;
+    the library then checks every sequence on the device.
+    """
+    qsl = getattr(md, "query_start_loc_cpu", None)
+    if qsl is None or len(qsl) != num_seqs + 1:
+        return -1
+    return sum(1 for i in range(num_seqs) if qsl[i + 1] - qsl[i] == 1)
+
+
 def paged_prefill_attention(q, kv_cache, md, scale):
     """Causal attention for a flattened varlen batch, reading K/V from the paged cache.
 
@@ -59,7 +71,7 @@ def paged_prefill_attention(q, kv_cache, md, scale):
         bt.data_ptr(), bt.stride(0), bt.shape[1],
         qsl.data_ptr(), seq_lens.data_ptr(), ctx_lens.data_ptr(), float(scale),
         out.data_ptr(), out.stride(0), out.stride(1),
-        num_seqs, num_tokens, int(md.max_query_len),
+        num_seqs, num_tokens, int(md.max_query_len), _single_query_seqs(md, num_seqs),
         num_heads, num_kv_heads, head_dim, page,
         _lib.stream_handle(q.device),
     )

@@ -144,9 +144,11 @@ extern "C" int bvllm_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_
                                    const int32_t* context_lens, float scale,
                                    void* out, int64_t out_stride_t, int64_t out_stride_h,
                                    int32_t num_seqs, int32_t num_tokens, int32_t max_query_len,
+                                   int32_t single_query_seqs,
                                    int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                    int32_t block_size, void* stream) {
   if (num_seqs < 0 || num_tokens < 0 || max_query_len < 0) return kBad;
+  if (single_query_seqs < -1 || single_query_seqs > num_seqs) return kBad;
   if (!valid_heads(num_heads, num_kv_heads)) return kBad;
   if (head_dim != 64 && head_dim != 128) return kBad;
   if (block_size != 16) return kBad;
@@ -158,6 +160,8 @@ extern "C" int bvllm_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_
       out_stride_h % 8)
     return kBad;
   if (max_blocks < 1 || bt_stride < max_blocks) return kBad;
+  // Offsets inside one page are 32-bit (decode kernel).
+  if ((int64_t)16 * cache_stride_tok > 0x7fffffff) return kBad;
 
   PrefillArgs a{};
   a.q = q; a.q_st = q_stride_t; a.q_sh = q_stride_h;
@@ -170,5 +174,6 @@ extern "C" int bvllm_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_
   a.out = out; a.o_st = out_stride_t; a.o_sh = out_stride_h;
   a.num_seqs = num_seqs; a.num_tokens = num_tokens; a.max_query_len = max_query_len;
   a.num_heads = num_heads; a.num_kv_heads = num_kv_heads; a.head_dim = head_dim;
+  a.single_query_seqs = single_query_seqs;
   return (int)paged_prefill(a, (hipStream_t)stream);
 }

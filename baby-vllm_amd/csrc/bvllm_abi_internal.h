@@ -36,6 +36,12 @@ struct DecodeArgs {
   int32_t num_splits, blocks_per_split;
   int32_t batch, num_heads, num_kv_heads, head_dim;
   int32_t waves;                           // waves per work-group (4 or 8; 0 = default)
+  // Prefill view (both null for a decode batch): row b is sequence b of a
+  // varlen prefill batch. Only sequences with exactly one query token are
+  // computed; their q / out row is query_start_loc[b] and they attend keys
+  // 0 .. min(seq_lens[b], context_lens[b] + 1) - 1.
+  const int32_t* query_start_loc;
+  const int32_t* context_lens;
 };
 
 struct PrefillArgs {
@@ -51,6 +57,9 @@ struct PrefillArgs {
   void* out;      int64_t o_st, o_sh;      // [T, H, D]
   int32_t num_seqs, num_tokens, max_query_len;
   int32_t num_heads, num_kv_heads, head_dim;
+  // Sequences with exactly one query token: -1 = unknown, 0 = none. When not 0
+  // those sequences run on the decode kernel and the prefill kernel skips them.
+  int32_t single_query_seqs;
 };
 
 hipError_t rope_kv_append(const RopeArgs& a, hipStream_t stream);
@@ -58,5 +67,7 @@ hipError_t paged_decode(const DecodeArgs& a, hipStream_t stream);
 // Partial states (per row and head) one decode launch writes to the workspace.
 int32_t decode_partials(const DecodeArgs& a);
 hipError_t paged_prefill(const PrefillArgs& a, hipStream_t stream);
+// The single-query sequences of a prefill batch, on the decode kernel (one pass).
+hipError_t decode_single_query_seqs(const PrefillArgs& a, hipStream_t stream);
 
 }  // namespace bvllm

@@ -173,7 +173,15 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
   const int g = lane >> 4;
   const int w = wave_id();
 
-  const int seq_len = uniform(a.seq_lens[b]);
+  int row = b;  // q / out row
+  int seq_len;
+  if (a.query_start_loc != nullptr) {
+    row = uniform(a.query_start_loc[b]);
+    if (uniform(a.query_start_loc[b + 1]) - row != 1) return;  // left to the prefill kernel
+    seq_len = min(uniform(a.seq_lens[b]), uniform(a.context_lens[b]) + 1);
+  } else {
+    seq_len = uniform(a.seq_lens[b]);
+  }
   int n_blocks = seq_len > 0 ? (seq_len + 15) / 16 : 0;
   n_blocks = min(n_blocks, a.max_blocks);
   const int start = split * a.blocks_per_split;
@@ -182,7 +190,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
   // Qᵀ operand: lane (n + 16g), chunk c -> q[b][kvh·G + n][8(4c+g) .. +8).
   uint4 qb[KC];
   {
-    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_sb +
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)row * a.q_sb +
                            (int64_t)(kvh * G + n) * a.q_sh;
 #pragma unroll
     for (int c = 0; c < KC; ++c) qb[c] = (n < G) ? ld16(qrow + 8 * (4 * c + g)) : make_uint4(0, 0, 0, 0);
@@ -295,7 +303,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
     if (L == 0.f) o = make_float4(0.f, 0.f, 0.f, 0.f);
     const int head = kvh * G + h;
     if (a.num_splits == 1) {
-      uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)b * a.o_sb + (int64_t)head * a.o_sh + d;
+      uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)row * a.o_sb + (int64_t)head * a.o_sh + d;
       uint2 pk;
       pk.x = pack_bf16x2_hw(o.x, o.y);
       pk.y = pack_bf16x2_hw(o.z, o.w);
@@ -484,6 +492,28 @@ static hipError_t decode_for_dim(const DecodeArgs& a, hipStream_t stream) {
 }
 
 int32_t decode_partials(const DecodeArgs& a) { return a.num_splits; }
+
+hipError_t decode_single_query_seqs(const PrefillArgs& p, hipStream_t stream) {
+  DecodeArgs a{};
+  a.q = p.q; a.q_sb = p.q_st; a.q_sh = p.q_sh;
+  a.k_cache = p.k_cache; a.v_cache = p.v_cache;
+  a.c_sb = p.c_sb; a.c_st = p.c_st; a.c_sh = p.c_sh;
+  a.num_pages = p.num_pages;
+  a.block_tables = p.block_tables; a.bt_stride = p.bt_stride; a.max_blocks = p.max_blocks;
+  a.seq_lens = p.seq_lens;
+  a.scale_log2 = p.scale_log2;
+  a.out = p.out; a.o_sb = p.o_st; a.o_sh = p.o_sh;
+  a.num_splits = 1; a.blocks_per_split = p.max_blocks;
+  a.batch = p.num_seqs; a.num_heads = p.num_heads; a.num_kv_heads = p.num_kv_heads; a.head_dim = p.head_dim;
+  a.waves = 4;
+  a.query_start_loc = p.query_start_loc;
+  a.context_lens = p.context_lens;
+  switch (p.head_dim) {
+    case 64: return launch_decode<64, 4, 2>(a, stream);
+    case 128: return launch_decode<128, 4, 2>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 hipError_t paged_decode(const DecodeArgs& a, hipStream_t stream) {
   DecodeArgs d = a;

@@ -56,6 +56,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   const int q_start = uniform(a.query_start_loc[s]);
   const int q_len = uniform(a.query_start_loc[s + 1]) - q_start;
   if (qb * QB >= q_len) return;
+  if (q_len == 1 && a.single_query_seqs != 0) return;  // on the decode kernel
   const int seq_len = uniform(a.seq_lens[s]);
   const int ctx = uniform(a.context_lens[s]);
   const int q_last = min(q_len, (qb + 1) * QB) - 1;
@@ -312,7 +313,14 @@ static hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Sequences with a single query token (decode rows of a mixed step) go to the
+// decode kernel, whose waves split the row's pages; the prefill kernel would
+// walk them with one live wave per work-group.
 hipError_t paged_prefill(const PrefillArgs& a, hipStream_t stream) {
+  if (a.single_query_seqs != 0) {
+    const hipError_t e = decode_single_query_seqs(a, stream);
+    if (e != hipSuccess || a.single_query_seqs == a.num_seqs) return e;
+  }
   switch (a.head_dim) {
     case 64: return launch_prefill<64, 4, 2>(a, stream);
     case 128: return launch_prefill<128, 4, 2>(a, stream);

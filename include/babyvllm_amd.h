@@ -37,7 +37,7 @@ extern "C" {
 #endif
 
 /* ABI version of this header; bumped on any signature change. */
-#define BVLLM_ABI_VERSION 2
+#define BVLLM_ABI_VERSION 3
 
 #if defined(__GNUC__)
 #define BVLLM_API __attribute__((visibility("default")))
@@ -118,6 +118,12 @@ BVLLM_API int bvllm_paged_decode(const void* q, int64_t q_stride_b, int64_t q_st
  * 0 .. context_lens[s] + i (and < seq_lens[s]) read from the cache through
  * block_tables[s]. K/V of the new tokens must already be in the cache.
  * max_query_len bounds every sequence's query count (it sizes the grid).
+ * single_query_seqs is the number of sequences with exactly one query token
+ * (decode rows of a mixed step), or -1 if the caller does not know it; when it
+ * is not 0 those sequences run on the decode kernel (a second launch on the
+ * same stream), which splits a row's pages over the waves of a work-group.
+ * Passing 0 when such sequences exist is allowed: the prefill kernel then
+ * computes them too.
  */
 BVLLM_API int bvllm_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                         const void* k_cache, const void* v_cache,
@@ -128,6 +134,7 @@ BVLLM_API int bvllm_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_s
                         const int32_t* context_lens, float scale,
                         void* out, int64_t out_stride_t, int64_t out_stride_h,
                         int32_t num_seqs, int32_t num_tokens, int32_t max_query_len,
+                        int32_t single_query_seqs,
                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                         int32_t block_size, void* stream);
 

@@ -78,7 +78,10 @@ def test_host_side_argument_rejection():
                                 None, 0, 0, None, 1, 1, 1, 28, 4, 128, 15, 0, None) == bad
     # head_dim 96
     assert h.bvllm_paged_prefill(None, 0, 0, None, None, 0, 0, 0, 0, None, 0, 0, None, None, None,
-                                 1.0, None, 0, 0, 1, 1, 1, 28, 4, 96, 16, None) == bad
+                                 1.0, None, 0, 0, 1, 1, 1, -1, 28, 4, 96, 16, None) == bad
+    # single_query_seqs above num_seqs
+    assert h.bvllm_paged_prefill(None, 0, 0, None, None, 0, 0, 0, 0, None, 0, 0, None, None, None,
+                                 1.0, None, 0, 0, 1, 1, 1, 2, 28, 4, 128, 16, None) == bad
     # 28 heads over 5 KV heads
     assert h.bvllm_rope_kv_append(None, 0, 0, None, 0, 0, None, 0, 0, None, 0, None, 0,
                                   None, None, 0, 0, 0, None, 1, 28, 5, 128, None) == bad

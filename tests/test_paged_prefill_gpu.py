@@ -106,3 +106,48 @@ def test_baseline_prefill_configs(name, specs):
     q, kv_cache, md = build_prefill_case(specs, 4, 7, 128, seed=len(specs))
     actual = _kernel()(q, kv_cache, md, 128 ** -0.5)
     assert_attn_close(actual, _oracle(q, kv_cache, md, 7))
+
+
+# ------------------------------------- single-query sequences on the decode kernel
+
+SINGLE_MIX = [(0, 40), (200, 1), (63, 1), (0, 1), (500, 1), (16, 16), (31, 1)]
+
+
+@pytest.mark.parametrize("hkv,group,d", [(4, 7, 128), (2, 7, 64)])
+def test_single_query_rows_whatever_the_host_hint(hkv, group, d, monkeypatch):
+    """Decode rows of a mixed step give oracle results whether the host passes
+    their count (decode kernel), -1 (decode kernel, rows found on the device)
+    or 0 (everything on the prefill kernel); the first two give the same bits."""
+    import babyvllm.kernels.paged_prefill as pp
+
+    q, kv_cache, md = build_prefill_case(SINGLE_MIX, hkv, group, d, seed=7)
+    expected = _oracle(q, kv_cache, md, group)
+    assert pp._single_query_seqs(md, len(SINGLE_MIX)) == 5
+    counted = _kernel()(q, kv_cache, md, d ** -0.5)
+    monkeypatch.setattr(pp, "_single_query_seqs", lambda md, n: -1)
+    unknown = _kernel()(q, kv_cache, md, d ** -0.5)
+    monkeypatch.setattr(pp, "_single_query_seqs", lambda md, n: 0)
+    prefill_only = _kernel()(q, kv_cache, md, d ** -0.5)
+    assert torch.equal(counted, unknown)
+    for out in (counted, prefill_only):
+        assert not torch.isnan(out).any()
+        assert_attn_close(out, expected)
+
+
+def test_step_of_only_single_query_rows():
+    q, kv_cache, md = build_prefill_case([(40, 1), (7, 1), (0, 1), (1000, 1)], 4, 7, 128, seed=3)
+    actual = _kernel()(q, kv_cache, md, 128 ** -0.5)
+    assert_attn_close(actual, _oracle(q, kv_cache, md, 7))
+
+
+def test_single_query_row_matches_paged_decode():
+    """A one-token sequence of a prefill step is the decode of that token."""
+    from babyvllm.kernels.paged_attn import paged_decode_attention
+
+    specs = [(300, 1), (0, 50), (129, 1)]
+    q, kv_cache, md = build_prefill_case(specs, 4, 7, 128, seed=11, nan_fill=False)
+    out = _kernel()(q, kv_cache, md, 128 ** -0.5)
+    rows = [0, 51]
+    dec = paged_decode_attention(q[rows].contiguous(), kv_cache, md.block_tables[[0, 2]].contiguous(),
+                                 md.seq_lens[[0, 2]].contiguous(), 128 ** -0.5, partition_blocks=0)
+    assert torch.equal(out[rows], dec)
