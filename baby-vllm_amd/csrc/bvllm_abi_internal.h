@@ -67,7 +67,5 @@ hipError_t paged_decode(const DecodeArgs& a, hipStream_t stream);
 // Partial states (per row and head) one decode launch writes to the workspace.
 int32_t decode_partials(const DecodeArgs& a);
 hipError_t paged_prefill(const PrefillArgs& a, hipStream_t stream);
-// The single-query sequences of a prefill batch, on the decode kernel (one pass).
-hipError_t decode_single_query_seqs(const PrefillArgs& a, hipStream_t stream);
 
 }  // namespace bvllm

@@ -16,14 +16,68 @@
 //                                         Sᵀ registers, Vᵀ element-picked from LDS rows)
 // Keys at or past hi = min(seq_len, ctx + last query + 1) are staged as zeros,
 // so cache slots that were never written (possibly NaN) never reach a product.
+//
+// Sequences with a single query token (the decode rows of a mixed step) are
+// instead computed by decode work-groups (paged_decode_wg.h) placed in front of
+// the prefill work-groups of the same launch: their waves split a row's pages,
+// where a prefill work-group would walk them with one live wave.
 #include "bvllm_device.h"
 #include "bvllm_abi_internal.h"
+#include "paged_decode_wg.h"
 
 namespace bvllm {
 
+// Query blocks of QB rows are numbered sequence by sequence, the blocks of a
+// sequence last (most keys) first; a sequence with one query token has none
+// when the decode work-groups compute it. Finds the sequence s and block qb of
+// number r, or returns false if r is past the last block. Every wave computes
+// the same wave-uniform answer (a scan of the per-sequence block counts).
+__device__ __forceinline__ bool find_query_block(const PrefillArgs& a, int QB, int r, int& s_out, int& qb_out) {
+  constexpr int kChunk = 4;  // 64-sequence slices whose counts are loaded together
+  const int lane = lane_id();
+  int before = 0;
+  for (int s0 = 0; s0 < a.num_seqs; s0 += 64 * kChunk) {
+    int nb[kChunk];
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      const int s = s0 + 64 * c + lane;
+      nb[c] = 0;
+      if (s < a.num_seqs) {
+        const int ql = a.query_start_loc[s + 1] - a.query_start_loc[s];
+        nb[c] = (ql == 1 && a.single_query_seqs != 0) ? 0 : (ql + QB - 1) / QB;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      int inc = nb[c];
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_up(inc, d, 64);
+        if (lane >= d) inc += t;
+      }
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(before + inc > r);
+      if (hit != 0) {
+        const int l = (int)__builtin_ctzll(hit);
+        const int nb_l = __shfl(nb[c], l, 64);
+        const int first = before + __shfl(inc, l, 64) - nb_l;
+        s_out = uniform(s0 + 64 * c + l);
+        qb_out = uniform(nb_l - 1 - (r - first));
+        return true;
+      }
+      before += __shfl(inc, 63, 64);
+    }
+  }
+  return false;
+}
+
+// Waves and pages in flight of the decode work-groups of a mixed step.
+constexpr int kDecodeWaves = 4;
+constexpr int kDecodeDepth = 2;
+
 template <int D, int NW, int QT>
-__global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a, int n_qb, int total_wg,
-                                                                  int per_xcd) {
+__global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a, int n_blocks_bound, int dense_qb,
+                                                                  int xcd_group, int per_xcd, DecodeArgs dec,
+                                                                  int n_dec_wgs) {
   constexpr int KT = 64;
   constexpr int PITCH = D + 8;  // bf16 elements; 16-byte pad keeps 16-row column reads conflict-free
   constexpr int KC = D / 32;
@@ -36,27 +90,63 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   static_assert(KT == 64, "a key tile spans four 16-token pages");
   typedef typename std::conditional<VD == 8, uint4, uint2>::type VRow;
 
-  __shared__ __attribute__((aligned(16))) uint16_t lds_k[2][KT * PITCH];
-  __shared__ __attribute__((aligned(16))) uint16_t lds_v[2][KT * PITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[4 * KT * PITCH];
+  uint16_t (*lds_k)[KT * PITCH] = reinterpret_cast<uint16_t (*)[KT * PITCH]>(lds);
+  uint16_t (*lds_v)[KT * PITCH] = reinterpret_cast<uint16_t (*)[KT * PITCH]>(lds + 2 * KT * PITCH);
+  static_assert(NW == kDecodeWaves, "decode work-groups run with the prefill work-group size");
+  static_assert(decode_lds_bytes<D, kDecodeWaves>(16) <= sizeof(lds), "decode work-group LDS");
 
-  // Work-groups are dispatched round-robin over the 8 XCDs; give each XCD a
-  // contiguous range of (sequence, KV head, query block) so the query blocks
-  // that share a prefix also share an L2.
-  const int id = blockIdx.x;
-  const int L = (id & 7) * per_xcd + (id >> 3);
-  if (L >= total_wg) return;
-  const int qb = n_qb - 1 - (L % n_qb);  // later (longer) query blocks first
-  const int sk = L / n_qb;
-  const int kvh = sk % a.num_kv_heads;
-  const int s = sk / a.num_kv_heads;
+  // The first n_dec_wgs work-groups (a multiple of 8) are decode work-groups,
+  // one per (sequence, KV head); those past the batch have nothing to do.
+  if ((int)blockIdx.x < n_dec_wgs) {
+    if ((int)blockIdx.x < dec.batch * dec.num_kv_heads)
+      decode_work_group<D, kDecodeWaves, kDecodeDepth>(dec, blockIdx.x, reinterpret_cast<float*>(lds));
+    return;
+  }
 
   const int G = a.num_heads / a.num_kv_heads;
   const int QP = 16 / G;
   const int QB = NW * QT * QP;
+
+  // Work-groups are dispatched round-robin over the 8 XCDs (XCD = id mod 8).
+  // xcd_group == -1 (many (sequence, KV head) pairs, dense numbering): each XCD
+  // takes a contiguous range of (sequence, KV head, block), so the blocks that
+  // share a prefix share an L2 and every XCD gets many whole pairs.
+  // xcd_group = 8 / Hkv > 0 (few pairs, or a mixed step): KV head h is served
+  // by XCDs h·xcd_group .. +xcd_group-1, which deal its query blocks out in
+  // boustrophedon order (0 1 | 1 0 | 0 1 ...): each L2 holds one KV head's
+  // keys, and the heavy-to-light run of a sequence's blocks spreads evenly.
+  const int id = blockIdx.x - n_dec_wgs;
+  int kvh, r;
+  if (xcd_group < 0) {
+    const int L = (id & 7) * per_xcd + (id >> 3);
+    if (L >= n_blocks_bound * a.num_kv_heads) return;
+    const int sk = L / dense_qb;
+    kvh = sk % a.num_kv_heads;
+    r = (sk / a.num_kv_heads) * dense_qb + (L - sk * dense_qb);
+  } else if (xcd_group > 0) {
+    const int x = id & 7;
+    const int j = id >> 3;
+    const int off = x % xcd_group;
+    kvh = x / xcd_group;
+    r = xcd_group * j + ((j & 1) ? xcd_group - 1 - off : off);
+  } else {
+    kvh = id % a.num_kv_heads;
+    r = id / a.num_kv_heads;
+  }
+  if (r >= n_blocks_bound) return;
+  int s, qb;
+  if (dense_qb > 0) {
+    // Dense numbering: every sequence owns dense_qb block numbers.
+    s = r / dense_qb;
+    qb = dense_qb - 1 - (r - s * dense_qb);
+  } else if (!find_query_block(a, QB, r, s, qb)) {
+    return;
+  }
   const int q_start = uniform(a.query_start_loc[s]);
   const int q_len = uniform(a.query_start_loc[s + 1]) - q_start;
   if (qb * QB >= q_len) return;
-  if (q_len == 1 && a.single_query_seqs != 0) return;  // on the decode kernel
+  if (q_len == 1 && a.single_query_seqs != 0) return;  // on the decode work-groups
   const int seq_len = uniform(a.seq_lens[s]);
   const int ctx = uniform(a.context_lens[s]);
   const int q_last = min(q_len, (qb + 1) * QB) - 1;
@@ -299,28 +389,63 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   }
 }
 
+// Decode view of a prefill batch: row b is sequence b; the decode work-group
+// computes it only if it has exactly one query token.
+static DecodeArgs single_query_view(const PrefillArgs& p) {
+  DecodeArgs a{};
+  a.q = p.q; a.q_sb = p.q_st; a.q_sh = p.q_sh;
+  a.k_cache = p.k_cache; a.v_cache = p.v_cache;
+  a.c_sb = p.c_sb; a.c_st = p.c_st; a.c_sh = p.c_sh;
+  a.num_pages = p.num_pages;
+  a.block_tables = p.block_tables; a.bt_stride = p.bt_stride; a.max_blocks = p.max_blocks;
+  a.seq_lens = p.seq_lens;
+  a.scale_log2 = p.scale_log2;
+  a.out = p.out; a.o_sb = p.o_st; a.o_sh = p.o_sh;
+  a.num_splits = 1; a.blocks_per_split = p.max_blocks;
+  a.batch = p.num_seqs; a.num_heads = p.num_heads; a.num_kv_heads = p.num_kv_heads; a.head_dim = p.head_dim;
+  a.waves = kDecodeWaves;
+  a.query_start_loc = p.query_start_loc;
+  a.context_lens = p.context_lens;
+  return a;
+}
+
 template <int D, int NW, int QT>
 static hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   const int G = a.num_heads / a.num_kv_heads;
-  const int QB = NW * QT * (16 / G);
-  const int n_qb = (a.max_query_len + QB - 1) / QB;
-  const int64_t total = (int64_t)n_qb * a.num_kv_heads * a.num_seqs;
-  if (total == 0) return hipSuccess;
-  if (total > 0x7ffffff0) return hipErrorInvalidValue;
-  const int per_xcd = (int)((total + 7) / 8);
-  hipLaunchKernelGGL((paged_prefill_kernel<D, NW, QT>), dim3((unsigned)(8 * per_xcd)), dim3(NW * 64), 0,
-                     stream, a, n_qb, (int)total, per_xcd);
+  const int64_t QB = NW * QT * (16 / G);
+  // Upper bound of the query-block count: Σ ceil(q_s / QB) ≤ (T + S·(QB-1)) / QB
+  // over the sequences the prefill work-groups compute.
+  int64_t T = a.num_tokens, S = a.num_seqs;
+  if (a.single_query_seqs > 0) {
+    T -= a.single_query_seqs;
+    S -= a.single_query_seqs;
+  }
+  int64_t bound = S > 0 ? (T + S * (QB - 1)) / QB : 0;
+  // Query blocks are numbered densely (ceil(max_query_len / QB) per sequence,
+  // found by division) unless that wastes more than a quarter of the grid on
+  // empty blocks, as in a mixed step; then compactly (found by a scan).
+  const int64_t dense = (a.max_query_len + QB - 1) / QB;
+  int dense_qb = 0;
+  if (dense * a.num_seqs * 4 <= bound * 5) {
+    dense_qb = (int)dense;
+    bound = dense * a.num_seqs;
+  }
+  int xcd_group = (a.num_kv_heads <= 8 && 8 % a.num_kv_heads == 0) ? 8 / a.num_kv_heads : 0;
+  if (dense_qb > 0 && (int64_t)a.num_seqs * a.num_kv_heads >= 64) xcd_group = -1;
+  const int64_t per_xcd = (bound * a.num_kv_heads + 7) / 8;
+  const int64_t prefill_wgs = xcd_group > 0 ? 8 * ((bound + xcd_group - 1) / xcd_group)
+                              : xcd_group < 0 ? 8 * per_xcd
+                                              : bound * a.num_kv_heads;
+  const int64_t dec_wgs = a.single_query_seqs != 0 ? ((int64_t)a.num_seqs * a.num_kv_heads + 7) / 8 * 8 : 0;
+  if (prefill_wgs + dec_wgs == 0) return hipSuccess;
+  if (prefill_wgs + dec_wgs > 0x7ffffff0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((paged_prefill_kernel<D, NW, QT>), dim3((unsigned)(dec_wgs + prefill_wgs)), dim3(NW * 64), 0,
+                     stream, a, (int)bound, dense_qb, xcd_group, (int)per_xcd, single_query_view(a),
+                     (int)dec_wgs);
   return hipGetLastError();
 }
 
-// Sequences with a single query token (decode rows of a mixed step) go to the
-// decode kernel, whose waves split the row's pages; the prefill kernel would
-// walk them with one live wave per work-group.
 hipError_t paged_prefill(const PrefillArgs& a, hipStream_t stream) {
-  if (a.single_query_seqs != 0) {
-    const hipError_t e = decode_single_query_seqs(a, stream);
-    if (e != hipSuccess || a.single_query_seqs == a.num_seqs) return e;
-  }
   switch (a.head_dim) {
     case 64: return launch_prefill<64, 4, 2>(a, stream);
     case 128: return launch_prefill<128, 4, 2>(a, stream);

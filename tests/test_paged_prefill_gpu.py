@@ -151,3 +151,35 @@ def test_single_query_row_matches_paged_decode():
     dec = paged_decode_attention(q[rows].contiguous(), kv_cache, md.block_tables[[0, 2]].contiguous(),
                                  md.seq_lens[[0, 2]].contiguous(), 128 ** -0.5, partition_blocks=0)
     assert torch.equal(out[rows], dec)
+
+
+# ------------------------------------------- work-group mapping (query-block list)
+
+def _many_seqs(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    specs = []
+    for i in range(n):
+        kind = i % 4
+        ctx = int(torch.randint(0, 200, (1,), generator=g))
+        q_len = [1, 2, int(torch.randint(3, 40, (1,), generator=g)), 0][kind]
+        specs.append((ctx, q_len))
+    return specs
+
+
+@pytest.mark.parametrize("n_seqs", [63, 64, 65, 300])
+def test_many_sequences_of_mixed_lengths(n_seqs):
+    """Covers the block-list scan across several 64-sequence slices, empty
+    sequences and single-query sequences between prefill ones."""
+    specs = _many_seqs(n_seqs, seed=n_seqs)
+    q, kv_cache, md = build_prefill_case(specs, 4, 7, 128, seed=n_seqs)
+    actual = _kernel()(q, kv_cache, md, 128 ** -0.5)
+    assert not torch.isnan(actual).any()
+    assert_attn_close(actual, _oracle(q, kv_cache, md, 7))
+
+
+@pytest.mark.parametrize("hkv,group,d", [(8, 2, 128), (1, 8, 128), (3, 2, 64), (16, 1, 64)])
+def test_kv_head_counts_and_xcd_groups(hkv, group, d):
+    specs = [(0, 70), (130, 1), (33, 45), (7, 1), (0, 16)]
+    q, kv_cache, md = build_prefill_case(specs, hkv, group, d, seed=hkv)
+    actual = _kernel()(q, kv_cache, md, d ** -0.5)
+    assert_attn_close(actual, _oracle(q, kv_cache, md, group))
