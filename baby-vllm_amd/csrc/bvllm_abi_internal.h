@@ -36,6 +36,7 @@ struct DecodeArgs {
   int32_t num_splits, blocks_per_split;
   int32_t batch, num_heads, num_kv_heads, head_dim;
   int32_t waves;                           // waves per work-group (4 or 8; 0 = default)
+  int32_t splits_per_wg;                   // consecutive splits one work-group computes (set by the launcher)
   // Prefill view (both null for a decode batch): row b is sequence b of a
   // varlen prefill batch. Only sequences with exactly one query token are
   // computed; their q / out row is query_start_loc[b] and they attend keys

@@ -20,107 +20,55 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
   decode_work_group<D, NW, PF>(a, blockIdx.x, smem);
 }
 
-// One work-group per (sequence, query head, 32-dim slice):
-//   out = Σ_s w_s·o_s / Σ_s w_s,  w_s = 2^(lse_s − max lse).
-// Thread (chunk, group) accumulates splits group, group + 32, ... in order, then
-// the 32 group sums are added in group order. The grouping depends only on the
-// split index, so trailing empty splits (w = 0, o = 0) leave the bits unchanged.
-template <int D>
-__global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeArgs a) {
-  constexpr int DS = 32;          // dims per work-group
-  constexpr int CH = DS / 4;      // float4 chunks per slice
-  constexpr int NG = 256 / CH;    // split groups
-  constexpr int SLICES = D / DS;
-  __shared__ float red[256];
-  __shared__ float4 gnum[NG][CH];
-  __shared__ float gden[NG];
+// Split reduce: out = Σ_s w_s·o_s / Σ_s w_s, w_s = 2^(lse_s − max lse), over the
+// S partial states of a (row, head). Both reduce kernels use the same
+// arithmetic, so a row's bits do not depend on S beyond its empty splits
+// (w = 0, o = 0; eager and graph launches differ only in those):
+//   * splits are taken in groups of kReduceGroup consecutive splits; a group's
+//     sums are fma chains in split order: num = fma(w_s, o_s, num), den += w_s;
+//   * group sums are added in group order, skipping groups with den == 0.
+// With S ≤ kReduceGroup there is one group and its chain is the result.
+constexpr int kReduceGroup = 32;
 
-  const int bh = blockIdx.x / SLICES;
-  const int d0 = (blockIdx.x % SLICES) * DS;
-  const int S = a.num_splits;
-  const float* lse = a.part_lse + (int64_t)bh * S;
-  const float* po = a.part_out + (int64_t)bh * S * D + d0;
+// One group's partial states for 4 dims, loaded in one round.
+struct ReduceGroup {
+  float l[kReduceGroup];
+  float4 x[kReduceGroup];
+};
 
-  float M = kNegInf;
-  for (int s = threadIdx.x; s < S; s += 256) M = fmaxf(M, lse[s]);
-  red[threadIdx.x] = M;
-  __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if ((int)threadIdx.x < off) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + off]);
-    __syncthreads();
-  }
-  M = red[0];
-  if (M == kNegInf) M = 0.f;
-
-  const int ch = threadIdx.x % CH;
-  const int grp = threadIdx.x / CH;
-  float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
-  float den = 0.f;
-#pragma unroll 4
-  for (int s = grp; s < S; s += NG) {
-    const float wgt = fast_exp2(lse[s] - M);
-    const float4 x = *reinterpret_cast<const float4*>(po + (int64_t)s * D + 4 * ch);
-    num.x += wgt * x.x;
-    num.y += wgt * x.y;
-    num.z += wgt * x.z;
-    num.w += wgt * x.w;
-    den += wgt;
-  }
-  gnum[grp][ch] = num;
-  if (ch == 0) gden[grp] = den;
-  __syncthreads();
-  if (grp == 0) {
-    float4 t = gnum[0][ch];
-    float dd = gden[0];
-    for (int q = 1; q < NG; ++q) {
-      const float4 x = gnum[q][ch];
-      t.x += x.x;
-      t.y += x.y;
-      t.z += x.z;
-      t.w += x.w;
-      dd += gden[q];
-    }
-    const float inv = 1.f / (dd == 0.f ? 1.f : dd);
-    const int b = bh / a.num_heads;
-    const int h = bh % a.num_heads;
-    uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d0 + 4 * ch;
-    uint2 pk;
-    pk.x = pack_bf16x2_hw(t.x * inv, t.y * inv);
-    pk.y = pack_bf16x2_hw(t.z * inv, t.w * inv);
-    st8(dst, pk);
+__device__ __forceinline__ void load_group(ReduceGroup& r, const float* lse, const float* po, int D, int s0,
+                                           int S) {
+#pragma unroll
+  for (int k = 0; k < kReduceGroup; ++k) {
+    const int s = s0 + k;
+    r.l[k] = s < S ? lse[s] : kNegInf;
+    r.x[k] = s < S ? *reinterpret_cast<const float4*>(po + (int64_t)s * D) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
 }
 
-// Reduce for at most 32 partial states per (row, head): one thread per
-// (row, head, 4 dims) accumulates the partials in order. With ≤ 32 partials
-// every group of decode_reduce_kernel holds at most one non-empty partial, so
-// both kernels return the same bits for the same row (trailing empty partials
-// add exact zeros in either).
-template <int D>
-__global__ __launch_bounds__(256) void decode_reduce_small_kernel(DecodeArgs a, int64_t items) {
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (t >= items) return;
-  const int64_t bh = t / (D / 4);
-  const int d = (int)(t - bh * (D / 4)) * 4;
-  const int S = a.num_splits;
-  const float* lse = a.part_lse + bh * S;
-  const float* po = a.part_out + bh * S * D + d;
+__device__ __forceinline__ float group_max(const ReduceGroup& r) {
   float M = kNegInf;
-#pragma unroll 8
-  for (int s = 0; s < S; ++s) M = fmaxf(M, lse[s]);
-  if (M == kNegInf) M = 0.f;
-  float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
-  float den = 0.f;
-#pragma unroll 8
-  for (int s = 0; s < S; ++s) {
-    const float wgt = fast_exp2(lse[s] - M);
-    const float4 x = *reinterpret_cast<const float4*>(po + (int64_t)s * D);
-    num.x += wgt * x.x;
-    num.y += wgt * x.y;
-    num.z += wgt * x.z;
-    num.w += wgt * x.w;
+#pragma unroll
+  for (int k = 0; k < kReduceGroup; ++k) M = fmaxf(M, r.l[k]);
+  return M;
+}
+
+// The group's fma chains in split order.
+__device__ __forceinline__ void chain_group(const ReduceGroup& r, float M, float4& num, float& den) {
+  num = make_float4(0.f, 0.f, 0.f, 0.f);
+  den = 0.f;
+#pragma unroll
+  for (int k = 0; k < kReduceGroup; ++k) {
+    const float wgt = fast_exp2(r.l[k] - M);
+    num.x = __builtin_fmaf(wgt, r.x[k].x, num.x);
+    num.y = __builtin_fmaf(wgt, r.x[k].y, num.y);
+    num.z = __builtin_fmaf(wgt, r.x[k].z, num.z);
+    num.w = __builtin_fmaf(wgt, r.x[k].w, num.w);
     den += wgt;
   }
+}
+
+__device__ __forceinline__ void store_reduced(const DecodeArgs& a, int64_t bh, int d, float4 num, float den) {
   const float inv = 1.f / (den == 0.f ? 1.f : den);
   const int b = (int)(bh / a.num_heads);
   const int h = (int)(bh % a.num_heads);
@@ -131,9 +79,104 @@ __global__ __launch_bounds__(256) void decode_reduce_small_kernel(DecodeArgs a, 
   st8(dst, pk);
 }
 
+// S ≤ kReduceGroup: one thread per (row, head, 4 dims), one group.
+template <int D>
+__global__ __launch_bounds__(256) void decode_reduce_small_kernel(DecodeArgs a, int64_t items) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= items) return;
+  const int64_t bh = t / (D / 4);
+  const int d = (int)(t - bh * (D / 4)) * 4;
+  const int S = a.num_splits;
+  ReduceGroup r;
+  load_group(r, a.part_lse + bh * S, a.part_out + bh * S * D + d, D, 0, S);
+  float M = group_max(r);
+  if (M == kNegInf) M = 0.f;
+  float4 num;
+  float den;
+  chain_group(r, M, num, den);
+  store_reduced(a, bh, d, num, den);
+}
+
+// S > kReduceGroup: one work-group per (row, head, 32-dim slice); thread
+// (chunk, q) sums group q of the current set of 32 groups, then the threads of
+// group 0 add the set's group sums in order onto the running total.
+template <int D>
+__global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeArgs a) {
+  constexpr int DS = 32;          // dims per work-group
+  constexpr int CH = DS / 4;      // float4 chunks per slice
+  constexpr int NQ = 256 / CH;    // groups per set
+  constexpr int SLICES = D / DS;
+  __shared__ float red[256];
+  __shared__ float4 gnum[NQ][CH];
+  static_assert(NQ <= 256, "max pass scratch");
+  __shared__ float gden[NQ];
+
+  const int64_t bh = blockIdx.x / SLICES;
+  const int d0 = (blockIdx.x % SLICES) * DS;
+  const int S = a.num_splits;
+  const float* lse = a.part_lse + bh * S;
+  const float* po = a.part_out + bh * S * D + d0;
+
+  const int ch = threadIdx.x % CH;
+  const int q = threadIdx.x / CH;
+  ReduceGroup r;
+  float M;
+  if (S <= NQ * kReduceGroup) {
+    // One set: the group loads double as the max pass.
+    load_group(r, lse, po + 4 * ch, D, q * kReduceGroup, S);
+    if (ch == 0) red[q] = group_max(r);
+    __syncthreads();
+    M = kNegInf;
+    for (int k = 0; k < NQ; ++k) M = fmaxf(M, red[k]);
+  } else {
+    M = kNegInf;
+    for (int s = threadIdx.x; s < S; s += 256) M = fmaxf(M, lse[s]);
+    red[threadIdx.x] = M;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+      if ((int)threadIdx.x < off) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + off]);
+      __syncthreads();
+    }
+    M = red[0];
+  }
+  if (M == kNegInf) M = 0.f;
+
+  float4 total = make_float4(0.f, 0.f, 0.f, 0.f);
+  float total_den = 0.f;
+  bool any = false;
+  for (int set0 = 0; set0 < S; set0 += NQ * kReduceGroup) {
+    if (set0 > 0 || S > NQ * kReduceGroup) load_group(r, lse, po + 4 * ch, D, set0 + q * kReduceGroup, S);
+    float4 num;
+    float den;
+    chain_group(r, M, num, den);
+    gnum[q][ch] = num;
+    if (ch == 0) gden[q] = den;
+    __syncthreads();
+    if (q == 0) {
+      for (int k = 0; k < NQ; ++k) {
+        if (gden[k] == 0.f) continue;
+        const float4 g = gnum[k][ch];
+        if (!any) {
+          total = g;
+          total_den = gden[k];
+          any = true;
+        } else {
+          total.x += g.x;
+          total.y += g.y;
+          total.z += g.z;
+          total.w += g.w;
+          total_den += gden[k];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (q == 0) store_reduced(a, bh, d0 + 4 * ch, total, total_den);
+}
+
 template <int D>
 static hipError_t launch_reduce(const DecodeArgs& r, hipStream_t stream) {
-  if (r.num_splits <= 32) {
+  if (r.num_splits <= kReduceGroup) {
     const int64_t items = (int64_t)r.batch * r.num_heads * (D / 4);
     hipLaunchKernelGGL((decode_reduce_small_kernel<D>), dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
                        stream, r, items);
@@ -144,8 +187,45 @@ static hipError_t launch_reduce(const DecodeArgs& r, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cached[dev] = v;
+  }
+  return cached[dev];
+}
+
+// Consecutive splits per work-group: about two work-groups per compute unit
+// when the plan has more (small splits of a short batch, e.g. 512 splits of 4
+// pages at batch 1: 4 splits per work-group, 33.7 instead of 37.5 us on
+// MI355X), so that each work-group streams several splits' pages back to back.
+// BVLLM_DECODE_SPLITS_PER_WG overrides the choice for tuning.
+static int decode_splits_per_wg(const DecodeArgs& a, int nw) {
+  if (a.num_splits <= 1 || a.blocks_per_split % nw != 0) return 1;
+  static const int forced = [] {
+    const char* e = getenv("BVLLM_DECODE_SPLITS_PER_WG");
+    return e ? atoi(e) : 0;
+  }();
+  int64_t gps;
+  if (forced > 0) {
+    gps = forced;
+  } else {
+    const int64_t cus = device_cus();
+    const int64_t total = (int64_t)a.batch * a.num_kv_heads * a.num_splits;
+    gps = (total + cus) / (2 * cus);
+  }
+  return (int)std::max<int64_t>(1, std::min<int64_t>(gps, a.num_splits));
+}
+
 template <int D, int NW, int PF>
-static hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
+static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
+  DecodeArgs a = args;
+  a.splits_per_wg = decode_splits_per_wg(a, NW);
   const int G = a.num_heads / a.num_kv_heads;
   const size_t smem = decode_lds_bytes<D, NW>(G);
   if (smem > 160 * 1024) return hipErrorInvalidValue;
@@ -156,7 +236,8 @@ static hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  const int64_t wgs = (int64_t)a.batch * a.num_kv_heads * a.num_splits;
+  const int64_t groups = (a.num_splits + a.splits_per_wg - 1) / a.splits_per_wg;
+  const int64_t wgs = (int64_t)a.batch * a.num_kv_heads * groups;
   if (wgs == 0) return hipSuccess;
   if (wgs > 0x7fffffff) return hipErrorInvalidValue;
   hipLaunchKernelGGL((paged_decode_kernel<D, NW, PF>), dim3((unsigned)wgs), dim3(NW * 64), smem, stream, a);

@@ -123,11 +123,14 @@ __device__ __forceinline__ void process_page(WaveState<D>& st, const PageRegs<D>
   mx = max_across_groups(mx);
   const float m_new = fmaxf(st.m, mx);
   // A page with no live token leaves the state bit-identical: m_new == m,
-  // alpha == 1 and p == 0 (the wave's first page always has a live token).
-  const float alpha = fast_exp2(st.m - m_new);
+  // alpha == 1 and p == 0. While no live token has been seen (m_new == -inf,
+  // e.g. a padding page that opens a split's state) 0 stands in for the max,
+  // so that alpha and p are 0 instead of exp2(-inf - -inf) = NaN.
+  const float m_ref = m_new == kNegInf ? 0.f : m_new;
+  const float alpha = fast_exp2(st.m - m_ref);
   float p[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) p[i] = fast_exp2(sv[i] - m_new);
+  for (int i = 0; i < 4; ++i) p[i] = fast_exp2(sv[i] - m_ref);
   st.l = st.l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
   st.m = m_new;
   if (!wave_all_one(alpha)) {  // x·1 == x: skipping is exact
@@ -158,6 +161,73 @@ __device__ __forceinline__ void process_page(WaveState<D>& st, const PageRegs<D>
 template <int D>
 constexpr int kTileBytes = 16 * (2 * D + 16);
 
+// Saves a wave's final state as a merge record: m[16], l[16], acc[G][D]
+// (row h of acc = head h of the group, un-normalised).
+template <int D>
+__device__ __forceinline__ void save_state(float* rec, const WaveState<D>& st, float l_tot, int G, int n, int g) {
+  constexpr int VD = D / 16;
+  constexpr int OD = D / 4;
+  if (g == 0) {
+    rec[n] = st.m;
+    rec[16 + n] = l_tot;
+  }
+  if (n < G) {
+    float* dst = rec + 32 + n * D + OD * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int c = 0; c < VD; ++c) dst[VD * i + c] = st.acc[c][i];
+    }
+  }
+}
+
+// Merges the NS wave states of one split in wave order (record s at
+// rec + s·rec_stride) and writes the bf16 output row (one split) or the split's
+// fp32 partial output and LSE. Thread `tid` of `nthreads` handles 4
+// consecutive dims of one head at a time.
+template <int D, int NS>
+__device__ __forceinline__ void merge_states(const DecodeArgs& a, const float* rec, int rec_stride, int G, int b,
+                                             int row, int kvh, int split, int tid, int nthreads) {
+  const int total4 = G * D / 4;
+  for (int e = tid; e < total4; e += nthreads) {
+    const int h = (e * 4) / D;
+    const int d = (e * 4) % D;
+    float M = kNegInf;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) M = fmaxf(M, rec[s * rec_stride + h]);
+    float L = 0.f;
+    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (M != kNegInf) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const float* ws = rec + s * rec_stride;
+        const float wgt = fast_exp2(ws[h] - M);
+        L = __builtin_fmaf(ws[16 + h], wgt, L);
+        const float4 x = *reinterpret_cast<const float4*>(ws + 32 + h * D + d);
+        A.x = __builtin_fmaf(x.x, wgt, A.x);
+        A.y = __builtin_fmaf(x.y, wgt, A.y);
+        A.z = __builtin_fmaf(x.z, wgt, A.z);
+        A.w = __builtin_fmaf(x.w, wgt, A.w);
+      }
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    float4 o = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
+    if (L == 0.f) o = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int head = kvh * G + h;
+    if (a.num_splits == 1) {
+      uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)row * a.o_sb + (int64_t)head * a.o_sh + d;
+      uint2 pk;
+      pk.x = pack_bf16x2_hw(o.x, o.y);
+      pk.y = pack_bf16x2_hw(o.z, o.w);
+      st8(dst, pk);
+    } else {
+      const int64_t prow = ((int64_t)b * a.num_heads + head) * a.num_splits + split;
+      *reinterpret_cast<float4*>(a.part_out + prow * D + d) = o;
+      if (d == 0) a.part_lse[prow] = (L > 0.f) ? M + __log2f(L) : kNegInf;
+    }
+  }
+}
+
 // LDS bytes one decode work-group uses: NW K transpose tiles, then NW merge
 // records of 32 + G·D floats.
 template <int D, int NW>
@@ -165,19 +235,29 @@ constexpr size_t decode_lds_bytes(int G) {
   return (size_t)NW * kTileBytes<D> + (size_t)NW * (32 + G * D) * sizeof(float);
 }
 
-// One decode work-group: (sequence, KV head, split) = wg, with NW waves and
-// `smem` pointing at decode_lds_bytes<D, NW>(G) bytes of LDS.
+// One decode work-group: (sequence, KV head, group of a.splits_per_wg
+// consecutive splits) = wg, with NW waves and `smem` pointing at
+// decode_lds_bytes<D, NW>(G) bytes of LDS. Each split's state is computed
+// exactly as a work-group of its own would (waves interleave the split's pages
+// from its first page, merge in wave order), so the bits do not depend on
+// splits_per_wg; the pages of the group's next split are already in flight
+// while a split is merged. splits_per_wg > 1 requires blocks_per_split % NW == 0,
+// so that wave w's pages of consecutive full splits continue one progression
+// (first page + w, stride NW) and all waves finish a full split together.
 template <int D, int NW, int PF>
 __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int wg, float* smem) {
   constexpr int KC = D / 32;
   constexpr int VD = D / 16;
-  constexpr int OD = D / 4;
 
   const int G = a.num_heads / a.num_kv_heads;
-  const int split = wg % a.num_splits;
-  const int bk = wg / a.num_splits;
+  const int gps = a.splits_per_wg;
+  const int n_groups = (a.num_splits + gps - 1) / gps;
+  const int grp = wg % n_groups;
+  const int bk = wg / n_groups;
   const int kvh = bk % a.num_kv_heads;
   const int b = bk / a.num_kv_heads;
+  const int j0 = grp * gps;
+  const int j1 = min(j0 + gps, a.num_splits);  // splits [j0, j1)
 
   const int lane = lane_id();
   const int n = lane & 15;
@@ -195,8 +275,11 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
   }
   int n_blocks = seq_len > 0 ? (seq_len + 15) / 16 : 0;
   n_blocks = min(n_blocks, a.max_blocks);
-  const int start = split * a.blocks_per_split;
-  const int end = (split == a.num_splits - 1) ? n_blocks : min(start + a.blocks_per_split, n_blocks);
+  const int bps = a.blocks_per_split;
+  const int start = j0 * bps;
+  // The last split of the row runs to the row's last page.
+  const int end = (j1 == a.num_splits) ? n_blocks : min(j1 * bps, n_blocks);
+  const int ppw = bps / NW;  // pages of a full split per wave (splits_per_wg > 1)
 
   // Qᵀ operand: lane (n + 16g), chunk c -> q[b][kvh·G + n][8(4c+g) .. +8).
   uint4 qb[KC];
@@ -208,15 +291,30 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
   }
 
   WaveState<D> st;
-  st.m = kNegInf;
-  st.l = 0.f;
+  auto reset = [&]() {
+    st.m = kNegInf;
+    st.l = 0.f;
 #pragma unroll
-  for (int c = 0; c < VD; ++c) st.acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < VD; ++c) st.acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  };
+  reset();
+
+  // Merge records (m[16], l[16], acc[G][D] per wave) follow the NW K tiles.
+  const int wstride = 32 + G * D;
+  float* merge = smem + NW * kTileBytes<D> / 4;
+  // Merges the NW wave states of split j in wave order and writes its result.
+  // Every wave calls it the same number of times.
+  auto finish_split = [&](int j) {
+    save_state<D>(merge + w * wstride, st, sum_across_groups(st.l), G, n, g);
+    __syncthreads();
+    merge_states<D, NW>(a, merge, wstride, G, b, row, kvh, j, threadIdx.x, NW * 64);
+    __syncthreads();  // records are rewritten by the next split
+    reset();
+  };
 
   uint32_t off[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) off[j] = (uint32_t)((4 * g + j) * a.c_st + VD * n);
-  // This wave's K transpose tile, then the per-wave merge records.
   unsigned char* tile = reinterpret_cast<unsigned char*>(smem) + w * kTileBytes<D>;
 
   const uint16_t* kc = reinterpret_cast<const uint16_t*>(a.k_cache) + (int64_t)kvh * a.c_sh;
@@ -225,6 +323,7 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
 
   const int first = start + w;
   const int cnt = (end > first) ? (end - first + NW - 1) / NW : 0;
+  int j_cur = j0;  // split the wave state belongs to
   // Lane k holds the table entry of this wave's page number base + k. The first
   // slice is requested together with seq_len and q (its index is clamped into
   // the row, so it does not wait for seq_len); entries past the row are unused.
@@ -240,25 +339,27 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
     // wave's range) and the page count is padded to a multiple of PF with fully
     // masked pages, so every wait counts exactly PF-1 younger pages.
     PageRegs<D> r[PF];
-    const uint16_t* kpage[PF];
-    const uint16_t* vpage[PF];
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int64_t p = phys(min(i, here - 1)) * a.c_sb;
       load_page<D>(r[i], kc + p, vc + p, off);
     }
-    (void)kpage;
-    (void)vpage;
     const int padded = (here + PF - 1) / PF * PF;
     for (int k = 0; k < padded; k += PF) {
 #pragma unroll
       for (int i = 0; i < PF; ++i) {
         wait_page<(PF - 1) * kLoadsPerPage, D>(r[i]);
-        const int page = first + NW * (base + k + i);
+        const int idx = base + k + i;
+        const int page = first + NW * idx;
         const int limit = (k + i < here) ? seq_len : 0;
         process_page<D>(st, r[i], qb, tile, n, g, page * 16 + 4 * g, limit, a.scale_log2);
         const int64_t pn = phys(min(k + i + PF, here - 1)) * a.c_sb;
         load_page<D>(r[i], kc + pn, vc + pn, off);
+        // End of a full split that is not the group's last: every wave is here.
+        if (gps > 1 && k + i < here && (idx + 1) % ppw == 0 && j_cur < j1 - 1 && (j_cur + 1) * bps <= n_blocks) {
+          finish_split(j_cur);
+          ++j_cur;
+        }
       }
     }
     // Drain: the loads issued for pages past the end must land before their
@@ -266,65 +367,9 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
 #pragma unroll
     for (int i = 0; i < PF; ++i) wait_page<0, D>(r[i]);
   }
-  const float l_tot = sum_across_groups(st.l);
-
-  // Merge the NW wave states in wave order. LDS layout per wave:
-  //   m[16], l[16], acc[G][D].
-  const int wstride = 32 + G * D;
-  float* merge = smem + NW * kTileBytes<D> / 4;
-  float* my = merge + w * wstride;
-  if (g == 0) {
-    my[n] = st.m;
-    my[16 + n] = l_tot;
-  }
-  if (n < G) {
-    float* dst = my + 32 + n * D + OD * g;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int c = 0; c < VD; ++c) dst[VD * i + c] = st.acc[c][i];
-    }
-  }
-  __syncthreads();
-
-  const int total4 = G * D / 4;
-  for (int e = threadIdx.x; e < total4; e += NW * 64) {
-    const int h = (e * 4) / D;
-    const int d = (e * 4) % D;
-    float M = kNegInf;
-#pragma unroll
-    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, merge[ww * wstride + h]);
-    float L = 0.f;
-    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (M != kNegInf) {
-#pragma unroll
-      for (int ww = 0; ww < NW; ++ww) {
-        const float* ws = merge + ww * wstride;
-        const float wgt = fast_exp2(ws[h] - M);
-        L += ws[16 + h] * wgt;
-        const float4 x = *reinterpret_cast<const float4*>(ws + 32 + h * D + d);
-        A.x += x.x * wgt;
-        A.y += x.y * wgt;
-        A.z += x.z * wgt;
-        A.w += x.w * wgt;
-      }
-    }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    float4 o = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
-    if (L == 0.f) o = make_float4(0.f, 0.f, 0.f, 0.f);
-    const int head = kvh * G + h;
-    if (a.num_splits == 1) {
-      uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)row * a.o_sb + (int64_t)head * a.o_sh + d;
-      uint2 pk;
-      pk.x = pack_bf16x2_hw(o.x, o.y);
-      pk.y = pack_bf16x2_hw(o.z, o.w);
-      st8(dst, pk);
-    } else {
-      const int64_t row = ((int64_t)b * a.num_heads + head) * a.num_splits + split;
-      *reinterpret_cast<float4*>(a.part_out + row * D + d) = o;
-      if (d == 0) a.part_lse[row] = (L > 0.f) ? M + __log2f(L) : kNegInf;
-    }
-  }
+  // The split holding the wave's last pages, then the group's splits that the
+  // row does not reach (zero output, -inf LSE).
+  for (; j_cur < j1; ++j_cur) finish_split(j_cur);
 }
 
 }  // namespace bvllm

@@ -404,6 +404,7 @@ static DecodeArgs single_query_view(const PrefillArgs& p) {
   a.num_splits = 1; a.blocks_per_split = p.max_blocks;
   a.batch = p.num_seqs; a.num_heads = p.num_heads; a.num_kv_heads = p.num_kv_heads; a.head_dim = p.head_dim;
   a.waves = kDecodeWaves;
+  a.splits_per_wg = 1;
   a.query_start_loc = p.query_start_loc;
   a.context_lens = p.context_lens;
   return a;

@@ -184,3 +184,23 @@ def test_baseline_decode_configs(batch, ctx):
     q, kv_cache, bt, seq_lens = make_decode_inputs(lens, width=cdiv(ctx, BLOCK_SIZE), seed=ctx + batch)
     actual = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=ctx)
     assert_attn_close(actual, _oracle(q, kv_cache, bt, lens, scale))
+
+
+@pytest.mark.parametrize("n", [600, 130, 2047])
+def test_reduce_bits_do_not_depend_on_the_split_count(n, monkeypatch):
+    """A row's bits depend only on its non-empty splits: an eager launch with
+    few splits (one reduce group) and a graph-bucket launch with more than 32
+    splits (several groups) agree bit for bit."""
+    from babyvllm.kernels.decode_split import DECODE_PARTITION_ENV, decode_split_plan
+
+    monkeypatch.delenv(DECODE_PARTITION_ENV, raising=False)
+    scale = HEAD_DIM ** -0.5
+    q, kv_cache, bt, seq_lens = make_decode_inputs([n], width=520, seed=n)
+    sms = torch.cuda.get_device_properties(0).multi_processor_count
+    s_eager, _ = decode_split_plan(1, 4, BLOCK_SIZE, 520, n, sms)
+    s_graph, _ = decode_split_plan(1, 4, BLOCK_SIZE, 520, 8192, sms)
+    assert s_eager <= 32 < s_graph or n > 32 * 4 * BLOCK_SIZE
+    eager = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=n)
+    graph = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=8192)
+    assert torch.equal(eager, graph)
+    assert_attn_close(graph, _oracle(q, kv_cache, bt, [n], scale))
