@@ -207,10 +207,8 @@ static int device_cus() {
 // BVLLM_DECODE_SPLITS_PER_WG overrides the choice for tuning.
 static int decode_splits_per_wg(const DecodeArgs& a, int nw) {
   if (a.num_splits <= 1 || a.blocks_per_split % nw != 0) return 1;
-  static const int forced = [] {
-    const char* e = getenv("BVLLM_DECODE_SPLITS_PER_WG");
-    return e ? atoi(e) : 0;
-  }();
+  const char* env = getenv("BVLLM_DECODE_SPLITS_PER_WG");  // read per launch: tests vary it
+  const int forced = env ? atoi(env) : 0;
   int64_t gps;
   if (forced > 0) {
     gps = forced;

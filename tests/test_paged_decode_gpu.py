@@ -204,3 +204,24 @@ def test_reduce_bits_do_not_depend_on_the_split_count(n, monkeypatch):
     graph = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=8192)
     assert torch.equal(eager, graph)
     assert_attn_close(graph, _oracle(q, kv_cache, bt, [n], scale))
+
+
+@pytest.mark.parametrize("lens", [[600, 37, 0], [2047, 1, 64], [130, 129, 128, 127]])
+def test_splits_per_work_group_do_not_change_bits(lens, monkeypatch):
+    """One work-group may compute several consecutive splits (its page loads
+    run on across split boundaries); every split's state, and so the output,
+    stays bit-identical. Rows ending inside a group make padding pages open a
+    split's state, which must leave it empty (not NaN)."""
+    from babyvllm.kernels.decode_split import DECODE_PARTITION_ENV
+
+    monkeypatch.delenv(DECODE_PARTITION_ENV, raising=False)
+    scale = HEAD_DIM ** -0.5
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, width=300, seed=len(lens))
+    outs = []
+    for gps in (1, 2, 3, 4, 8):
+        monkeypatch.setenv("BVLLM_DECODE_SPLITS_PER_WG", str(gps))
+        outs.append(_kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=4096, partition_blocks=4))
+    for out in outs[1:]:
+        assert torch.equal(out, outs[0])
+    assert not torch.isnan(outs[0]).any()
+    assert_attn_close(outs[0], _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
