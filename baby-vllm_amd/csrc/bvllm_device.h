@@ -96,6 +96,17 @@ __device__ __forceinline__ T uniform(T v) {
   return (T)__builtin_amdgcn_readfirstlane((int)v);
 }
 
+// LDS transpose read (ds_read_b64_tr_b16, 8-byte aligned LDS address): within
+// each 16-lane group, lane l receives element (l mod 4) of the 4 bf16 that lanes
+// 4i + l/4 (i < 4) address, as its element i. So if lane s of group g addresses
+// row r0 + 4g + s/4, columns c0 + 4(s mod 4) .. +3 of a row-major bf16 matrix,
+// lane l gets column c0 + l of rows r0 + 4g + i, i < 4: a column operand for MFMA.
+__device__ __forceinline__ uint2 ld_tr16(const uint16_t* lds_ptr) {
+  typedef __attribute__((address_space(3))) i16x4_t* LdsVec;
+  const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsVec)(lds_ptr));
+  return __builtin_bit_cast(uint2, v);
+}
+
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ uint2 ld8(const void* p) { return *reinterpret_cast<const uint2*>(p); }
 __device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }

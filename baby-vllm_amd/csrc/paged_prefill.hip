@@ -13,7 +13,7 @@
 // buffered: the global loads of tile t+1 are in flight while tile t computes.
 //   Sᵀ[16 keys × 16 cols] = K · Qᵀ       (mfma 16x16x32, K operand from LDS)
 //   Oᵀ[D × 16 cols]      += Vᵀ · Pᵀ      (mfma 16x16x32 over 32 keys, Pᵀ from the
-//                                         Sᵀ registers, Vᵀ element-picked from LDS rows)
+//                                         Sᵀ registers, Vᵀ by LDS transpose reads)
 // Keys at or past hi = min(seq_len, ctx + last query + 1) are staged as zeros,
 // so cache slots that were never written (possibly NaN) never reach a product.
 //
@@ -79,20 +79,22 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
                                                                   int xcd_group, int per_xcd, DecodeArgs dec,
                                                                   int n_dec_wgs) {
   constexpr int KT = 64;
-  constexpr int PITCH = D + 8;  // bf16 elements; 16-byte pad keeps 16-row column reads conflict-free
+  // LDS row pitches (bf16 elements): K rows are read 16 B per lane from 16
+  // rows (a 16-byte pad spreads them over all banks); V rows are read by
+  // transpose reads, 32 B from each of 4 rows per 16 lanes (a 32-byte pad).
+  constexpr int PITCH = D + 8;
+  constexpr int PITCH_V = D + 16;
   constexpr int KC = D / 32;
   constexpr int VD = D / 16;
-  constexpr int OD = D / 4;
   constexpr int CPR = D / 8;
   constexpr int CHUNKS = KT * CPR;
   constexpr int PER_T = CHUNKS / (NW * 64);
   static_assert(PER_T * NW * 64 == CHUNKS, "tile chunks must divide evenly over the work-group");
   static_assert(KT == 64, "a key tile spans four 16-token pages");
-  typedef typename std::conditional<VD == 8, uint4, uint2>::type VRow;
 
-  __shared__ __attribute__((aligned(16))) uint16_t lds[4 * KT * PITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * KT * PITCH + 2 * KT * PITCH_V];
   uint16_t (*lds_k)[KT * PITCH] = reinterpret_cast<uint16_t (*)[KT * PITCH]>(lds);
-  uint16_t (*lds_v)[KT * PITCH] = reinterpret_cast<uint16_t (*)[KT * PITCH]>(lds + 2 * KT * PITCH);
+  uint16_t (*lds_v)[KT * PITCH_V] = reinterpret_cast<uint16_t (*)[KT * PITCH_V]>(lds + 2 * KT * PITCH);
   static_assert(NW == kDecodeWaves, "decode work-groups run with the prefill work-group size");
   static_assert(decode_lds_bytes<D, kDecodeWaves>(16) <= sizeof(lds), "decode work-group LDS");
 
@@ -247,7 +249,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
       const int key = e / CPR;
       const int part = e - key * CPR;
       st16(&lds_k[buf][key * PITCH + part * 8], stk[r]);
-      st16(&lds_v[buf][key * PITCH + part * 8], stv[r]);
+      st16(&lds_v[buf][key * PITCH_V + part * 8], stv[r]);
     }
   };
 
@@ -334,25 +336,17 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
         }
       }
 
+      // Vᵀ operand of dims 16c .. 16c+15 over keys 32u + {4g .. 4g+3, 16+4g .. 16+4g+3}
+      // (the keys whose P this lane holds): two transpose reads.
+      const int trow = 4 * g + (n >> 2);
+      const int tcol = 4 * (n & 3);
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        VRow vr[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int key = 16 * (2 * u + j / 4) + 4 * g + (j & 3);
-          if constexpr (VD == 8) vr[j] = ld16(V + key * PITCH + VD * n);
-          else vr[j] = ld8(V + key * PITCH + VD * n);
-        }
 #pragma unroll
         for (int c = 0; c < VD; ++c) {
-          uint32_t d[4];
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&vr[2 * jj]);
-            const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&vr[2 * jj + 1]);
-            d[jj] = pick_halves(r0[c / 2], r1[c / 2], c & 1);
-          }
-          const uint4 va = make_uint4(d[0], d[1], d[2], d[3]);
+          const uint2 lo = ld_tr16(V + (32 * u + trow) * PITCH_V + 16 * c + tcol);
+          const uint2 hi = ld_tr16(V + (32 * u + 16 + trow) * PITCH_V + 16 * c + tcol);
+          const uint4 va = make_uint4(lo.x, lo.y, hi.x, hi.y);
 #pragma unroll
           for (int ct = 0; ct < QT; ++ct) acc[ct][c] = mfma_16x16x32(va, pb[ct][u], acc[ct][c]);
         }
@@ -368,23 +362,15 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
     const float lt = sum_across_groups(l[ct]);
     if (!valid[ct]) continue;
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    // acc[ct][c][i] is dim 16c + 4g + i.
     uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + (int64_t)(q_start + qi[ct]) * a.o_st +
-                     (int64_t)(kvh * G + hl) * a.o_sh + OD * g;
+                     (int64_t)(kvh * G + hl) * a.o_sh + 4 * g;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (VD == 8) {
-        uint4 pk;
-        pk.x = pack_bf16x2_hw(acc[ct][0][i] * inv, acc[ct][1][i] * inv);
-        pk.y = pack_bf16x2_hw(acc[ct][2][i] * inv, acc[ct][3][i] * inv);
-        pk.z = pack_bf16x2_hw(acc[ct][4][i] * inv, acc[ct][5][i] * inv);
-        pk.w = pack_bf16x2_hw(acc[ct][6][i] * inv, acc[ct][7][i] * inv);
-        st16(orow + VD * i, pk);
-      } else {
-        uint2 pk;
-        pk.x = pack_bf16x2_hw(acc[ct][0][i] * inv, acc[ct][1][i] * inv);
-        pk.y = pack_bf16x2_hw(acc[ct][2][i] * inv, acc[ct][3][i] * inv);
-        st8(orow + VD * i, pk);
-      }
+    for (int c = 0; c < VD; ++c) {
+      uint2 pk;
+      pk.x = pack_bf16x2_hw(acc[ct][c][0] * inv, acc[ct][c][1] * inv);
+      pk.y = pack_bf16x2_hw(acc[ct][c][2] * inv, acc[ct][c][3] * inv);
+      st8(orow + 16 * c, pk);
     }
   }
 }
