@@ -291,11 +291,13 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
       const bool diag = (kt * KT + KT - 1 > ctx + wave_q0) || (kt * KT + KT > hi);
 #pragma unroll
       for (int ct = 0; ct < QT; ++ct) {
+        // Raw scores; the scale (> 0, so the max commutes with it) is applied
+        // inside the exponent's fma: p = 2^(s·scale_log2 − m).
         float sv[4][4];
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) sv[t][i] = sacc[ct][t][i] * a.scale_log2;
+          for (int i = 0; i < 4; ++i) sv[t][i] = sacc[ct][t][i];
         if (diag) {
 #pragma unroll
           for (int t = 0; t < 4; ++t)
@@ -310,17 +312,17 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
         for (int t = 0; t < 4; ++t)
           mx = fmaxf(mx, fmaxf(fmaxf(sv[t][0], sv[t][1]), fmaxf(sv[t][2], sv[t][3])));
         mx = max_across_groups(mx);
-        const float m_new = fmaxf(m[ct], mx);
+        const float m_new = fmaxf(m[ct], mx * a.scale_log2);
         const float alpha = fast_exp2(m[ct] - m_new);
         float p[4][4];
-        float psum = 0.f;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            p[t][i] = fast_exp2(sv[t][i] - m_new);
-            psum += p[t][i];
-          }
+          for (int i = 0; i < 4; ++i) p[t][i] = fast_exp2(__builtin_fmaf(sv[t][i], a.scale_log2, -m_new));
+        float ps[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) ps[t] = (p[t][0] + p[t][1]) + (p[t][2] + p[t][3]);
+        const float psum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
         l[ct] = l[ct] * alpha + psum;
         m[ct] = m_new;
         if (!wave_all_one(alpha)) {  // x·1 == x: skipping is exact
