@@ -60,9 +60,23 @@ SIGNATURES = {
         _i32, _i32, _i32, _i32,     # H, Hkv, D, block_size
         _p,                         # stream
     ]),
+    "bvllm_argmax_workspace_bytes": (ctypes.c_int64, [_i32, _i32]),
+    "bvllm_greedy_argmax": (ctypes.c_int, [
+        _p, _i64, _i32, _i32,       # logits, row_stride, rows, vocab
+        _i32, _p, _p,               # logits_fp32, workspace, out
+        _p,                         # stream
+    ]),
+    "bvllm_fused_add_rms_norm": (ctypes.c_int, [
+        _p, _i64, _p, _i64,         # input, stride, residual, stride
+        _p, _i32,                   # weight, weight_fp32
+        _p, _i64,                   # out, stride
+        _i32, _i32, _f32,           # rows, hidden, eps
+        _p,                         # stream
+    ]),
+    "bvllm_silu_mul": (ctypes.c_int, [_p, _i64, _i32, _p, _p]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class KernelLibraryError(RuntimeError):

@@ -177,3 +177,55 @@ extern "C" int bvllm_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_
   a.single_query_seqs = single_query_seqs;
   return (int)paged_prefill(a, (hipStream_t)stream);
 }
+
+extern "C" int64_t bvllm_argmax_workspace_bytes(int32_t rows, int32_t vocab) {
+  if (rows <= 0 || vocab <= 0) return 0;
+  return argmax_workspace_bytes(rows, vocab);
+}
+
+extern "C" int bvllm_greedy_argmax(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                                   int32_t logits_fp32, void* workspace, int64_t* out, void* stream) {
+  if (rows < 0 || vocab < 1 || (logits_fp32 != 0 && logits_fp32 != 1)) return kBad;
+  if (rows == 0) return 0;
+  if (!logits || !out || !workspace || row_stride < vocab) return kBad;
+  if (((uintptr_t)workspace & 3u) != 0) return kBad;
+  ArgmaxArgs a{};
+  a.logits = logits; a.row_stride = row_stride;
+  a.rows = rows; a.vocab = vocab;
+  a.fp32 = logits_fp32;
+  const int64_t esize = logits_fp32 ? 4 : 2;
+  a.vec_ok = aligned16(logits) && (row_stride * esize) % 16 == 0 && ((int64_t)vocab * esize) % 16 == 0;
+  a.workspace = workspace;
+  a.out = out;
+  return (int)greedy_argmax(a, (hipStream_t)stream);
+}
+
+extern "C" int bvllm_fused_add_rms_norm(const void* input, int64_t input_stride, void* residual,
+                                        int64_t residual_stride, const void* weight, int32_t weight_fp32,
+                                        void* out, int64_t out_stride, int32_t rows, int32_t hidden, float eps,
+                                        void* stream) {
+  if (rows < 0 || hidden < 1 || (weight_fp32 != 0 && weight_fp32 != 1)) return kBad;
+  if (rows == 0) return 0;
+  if (!input || !weight || !out || input_stride < hidden || out_stride < hidden) return kBad;
+  if (residual && residual_stride < hidden) return kBad;
+  NormArgs a{};
+  a.input = input; a.in_stride = input_stride;
+  a.residual = residual; a.res_stride = residual_stride;
+  a.weight = weight; a.weight_fp32 = weight_fp32;
+  a.out = out; a.out_stride = out_stride;
+  a.rows = rows; a.n = hidden; a.eps = eps;
+  a.vec_ok = hidden % 8 == 0 && aligned16(input) && aligned16(out) && aligned16(weight) &&
+             input_stride % 8 == 0 && out_stride % 8 == 0 &&
+             (!residual || (aligned16(residual) && residual_stride % 8 == 0));
+  return (int)fused_add_rms_norm(a, (hipStream_t)stream);
+}
+
+extern "C" int bvllm_silu_mul(const void* gate_up, int64_t rows, int32_t d, void* out, void* stream) {
+  if (rows < 0 || d < 1) return kBad;
+  if (rows == 0) return 0;
+  if (!gate_up || !out) return kBad;
+  SiluArgs a{};
+  a.gate_up = gate_up; a.out = out; a.rows = rows; a.d = d;
+  a.vec_ok = d % 8 == 0 && aligned16(gate_up) && aligned16(out);
+  return (int)silu_mul(a, (hipStream_t)stream);
+}

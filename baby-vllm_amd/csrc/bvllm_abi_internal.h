@@ -63,7 +63,39 @@ struct PrefillArgs {
   int32_t single_query_seqs;
 };
 
+struct ArgmaxArgs {
+  const void* logits; int64_t row_stride;  // [rows, vocab], unit column stride
+  int32_t rows, vocab;
+  int32_t fp32;                            // 1: fp32 logits, 0: bf16
+  int32_t vec_ok;                          // 16-byte loads cover whole rows exactly
+  void* workspace;                         // argmax_workspace_bytes(rows, vocab)
+  int64_t* out;                            // [rows]
+};
+
+struct NormArgs {
+  const void* input; int64_t in_stride;    // [rows, n] bf16
+  void* residual;    int64_t res_stride;   // [rows, n] bf16 or null; receives input + residual
+  const void* weight;                      // [n], bf16 or fp32
+  int32_t weight_fp32;
+  void* out;         int64_t out_stride;   // [rows, n] bf16
+  int32_t rows, n;
+  float eps;
+  int32_t vec_ok;                          // 16-byte aligned rows, n % 8 == 0
+};
+
+struct SiluArgs {
+  const void* gate_up;                     // [rows, 2d] bf16, contiguous
+  void* out;                               // [rows, d] bf16, contiguous
+  int64_t rows;
+  int32_t d;
+  int32_t vec_ok;                          // 16-byte aligned, d % 8 == 0
+};
+
 hipError_t rope_kv_append(const RopeArgs& a, hipStream_t stream);
+int64_t argmax_workspace_bytes(int32_t rows, int32_t vocab);
+hipError_t greedy_argmax(const ArgmaxArgs& a, hipStream_t stream);
+hipError_t fused_add_rms_norm(const NormArgs& a, hipStream_t stream);
+hipError_t silu_mul(const SiluArgs& a, hipStream_t stream);
 hipError_t paged_decode(const DecodeArgs& a, hipStream_t stream);
 // Partial states (per row and head) one decode launch writes to the workspace.
 int32_t decode_partials(const DecodeArgs& a);

@@ -1,0 +1,219 @@
+// Fused residual add + RMSNorm, and SiLU(gate)·up: the two elementwise /
+// row-reduction kernels of a decoder layer, both HBM-bound.
+//
+// fused_add_rms_norm replaces _fused_add_rms_norm_kernel
+// (babyvllm/kernels/layernorm.py:5-83):
+//   x = input (+ residual, rounded to bf16; the sum is written back to residual)
+//   out = bf16( bf16(x · rsqrt(mean(x²) + eps)) · w )        (w bf16 or fp32)
+// One wave per row: 16-byte loads, the row kept in registers between the sum
+// of squares (fp32, wave reduction) and the scaling. Rows wider than the
+// register budget, or not 16-byte aligned, take a two-pass scalar kernel.
+//
+// fused_silu_mul replaces _silu_mul_kernel (babyvllm/kernels/activation.py:5-65):
+//   out[r, c] = bf16( silu(g) · u ),  g = gate_up[r, c], u = gate_up[r, D + c],
+//   silu(g) = g · (1 / (1 + e^{-g})) in fp32, one rounding at the end.
+#include "bvllm_device.h"
+#include "bvllm_abi_internal.h"
+
+namespace bvllm {
+
+namespace {
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+__device__ __forceinline__ float add_bf16(float a, float b) { return bf16_to_f32(f32_to_bf16_rne(a + b)); }
+
+__device__ __forceinline__ uint16_t norm_out(float x, float r, float w) {
+  return (uint16_t)f32_to_bf16_rne(bf16_to_f32(f32_to_bf16_rne(x * r)) * w);
+}
+
+template <bool W32>
+__device__ __forceinline__ float weight_at(const void* w, int i) {
+  if constexpr (W32) return reinterpret_cast<const float*>(w)[i];
+  else return bf16_to_f32(reinterpret_cast<const uint16_t*>(w)[i]);
+}
+
+// CPL: 16-byte chunks (8 bf16) per lane; the row has n ≤ 64·CPL·8 elements.
+template <int CPL, bool HAS_RES, bool W32>
+__global__ __launch_bounds__(256) void rms_norm_vec_kernel(NormArgs a) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const int lane = threadIdx.x & 63;
+  const int chunks = a.n / 8;
+  const uint16_t* in = reinterpret_cast<const uint16_t*>(a.input) + (int64_t)row * a.in_stride;
+  uint16_t* res = reinterpret_cast<uint16_t*>(a.residual) + (int64_t)row * a.res_stride;
+  uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + (int64_t)row * a.out_stride;
+
+  uint4 xv[CPL];
+  uint4 rv[CPL];
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const int c = lane + 64 * k;
+    xv[k] = c < chunks ? ld16(in + 8 * c) : make_uint4(0, 0, 0, 0);
+    if (HAS_RES) rv[k] = c < chunks ? ld16(res + 8 * c) : make_uint4(0, 0, 0, 0);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    uint32_t* xw = reinterpret_cast<uint32_t*>(&xv[k]);
+    if (HAS_RES) {
+      const uint32_t* rw = reinterpret_cast<const uint32_t*>(&rv[k]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        xw[q] = pack_bf16x2(add_bf16(lo_f32(xw[q]), lo_f32(rw[q])), add_bf16(hi_f32(xw[q]), hi_f32(rw[q])));
+      const int c = lane + 64 * k;
+      if (c < chunks) st16(res + 8 * c, xv[k]);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float l = lo_f32(xw[q]), h = hi_f32(xw[q]);
+      ss = __builtin_fmaf(l, l, ss);
+      ss = __builtin_fmaf(h, h, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = 1.f / sqrtf(ss / (float)a.n + a.eps);
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const int c = lane + 64 * k;
+    if (c >= chunks) continue;
+    const uint32_t* xw = reinterpret_cast<const uint32_t*>(&xv[k]);
+    float w[8];
+    if constexpr (W32) {
+      const float* wp = reinterpret_cast<const float*>(a.weight) + 8 * c;
+      const uint4 w0 = ld16(wp), w1 = ld16(wp + 4);
+      const float* f0 = reinterpret_cast<const float*>(&w0);
+      const float* f1 = reinterpret_cast<const float*>(&w1);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        w[q] = f0[q];
+        w[4 + q] = f1[q];
+      }
+    } else {
+      const uint4 wv = ld16(reinterpret_cast<const uint16_t*>(a.weight) + 8 * c);
+      const uint32_t* ww = reinterpret_cast<const uint32_t*>(&wv);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        w[2 * q] = lo_f32(ww[q]);
+        w[2 * q + 1] = hi_f32(ww[q]);
+      }
+    }
+    uint4 o;
+    uint32_t* ow = reinterpret_cast<uint32_t*>(&o);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      ow[q] = (uint32_t)norm_out(lo_f32(xw[q]), r, w[2 * q]) | ((uint32_t)norm_out(hi_f32(xw[q]), r, w[2 * q + 1]) << 16);
+    st16(out + 8 * c, o);
+  }
+}
+
+// Any n and stride: one wave per row, two passes (the residual sum is written
+// in the first and read back in the second).
+template <bool HAS_RES, bool W32>
+__global__ __launch_bounds__(256) void rms_norm_scalar_kernel(NormArgs a) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const int lane = threadIdx.x & 63;
+  const uint16_t* in = reinterpret_cast<const uint16_t*>(a.input) + (int64_t)row * a.in_stride;
+  uint16_t* res = reinterpret_cast<uint16_t*>(a.residual) + (int64_t)row * a.res_stride;
+  uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + (int64_t)row * a.out_stride;
+  float ss = 0.f;
+  for (int i = lane; i < a.n; i += 64) {
+    float x = bf16_to_f32(in[i]);
+    if (HAS_RES) {
+      x = add_bf16(x, bf16_to_f32(res[i]));
+      res[i] = (uint16_t)f32_to_bf16_rne(x);
+    }
+    ss = __builtin_fmaf(x, x, ss);
+  }
+  ss = wave_sum(ss);
+  const float r = 1.f / sqrtf(ss / (float)a.n + a.eps);
+  const uint16_t* src = HAS_RES ? res : in;
+  for (int i = lane; i < a.n; i += 64) out[i] = norm_out(bf16_to_f32(src[i]), r, weight_at<W32>(a.weight, i));
+}
+
+template <int CPL>
+hipError_t launch_norm_vec(const NormArgs& a, dim3 grid, hipStream_t s) {
+  const bool res = a.residual != nullptr;
+  if (res && a.weight_fp32) hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, true, true>), grid, dim3(256), 0, s, a);
+  else if (res) hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, true, false>), grid, dim3(256), 0, s, a);
+  else if (a.weight_fp32) hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, false, true>), grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, false, false>), grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+// Vector form: 8 gate and 8 up elements per thread.
+__global__ __launch_bounds__(256) void silu_mul_vec_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ out,
+                                                           int64_t total_chunks, int d_chunks) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= total_chunks) return;
+  const int64_t row = t / d_chunks;
+  const int c = (int)(t - row * d_chunks);
+  const uint16_t* g = gu + row * (int64_t)d_chunks * 16 + 8 * c;
+  const uint4 gv = ld16(g);
+  const uint4 uv = ld16(g + (int64_t)d_chunks * 8);
+  const uint32_t* gw = reinterpret_cast<const uint32_t*>(&gv);
+  const uint32_t* uw = reinterpret_cast<const uint32_t*>(&uv);
+  uint4 o;
+  uint32_t* ow = reinterpret_cast<uint32_t*>(&o);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float g0 = lo_f32(gw[q]), g1 = hi_f32(gw[q]);
+    const float s0 = g0 * (1.f / (1.f + expf(-g0))), s1 = g1 * (1.f / (1.f + expf(-g1)));
+    ow[q] = pack_bf16x2(s0 * lo_f32(uw[q]), s1 * hi_f32(uw[q]));
+  }
+  st16(out + row * (int64_t)d_chunks * 8 + 8 * c, o);
+}
+
+__global__ __launch_bounds__(256) void silu_mul_scalar_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ out,
+                                                              int64_t total, int d) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= total) return;
+  const int64_t row = t / d;
+  const int c = (int)(t - row * d);
+  const float g = bf16_to_f32(gu[row * 2 * d + c]);
+  const float u = bf16_to_f32(gu[row * 2 * d + d + c]);
+  out[t] = (uint16_t)f32_to_bf16_rne(g * (1.f / (1.f + expf(-g))) * u);
+}
+
+}  // namespace
+
+hipError_t fused_add_rms_norm(const NormArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)((a.rows + 3) / 4));
+  if (a.vec_ok) {
+    const int chunks = a.n / 8;
+    if (chunks <= 64 * 2) return launch_norm_vec<2>(a, grid, s);
+    if (chunks <= 64 * 4) return launch_norm_vec<4>(a, grid, s);
+    if (chunks <= 64 * 8) return launch_norm_vec<8>(a, grid, s);
+    if (chunks <= 64 * 16) return launch_norm_vec<16>(a, grid, s);
+  }
+  const bool res = a.residual != nullptr;
+  if (res && a.weight_fp32) hipLaunchKernelGGL((rms_norm_scalar_kernel<true, true>), grid, dim3(256), 0, s, a);
+  else if (res) hipLaunchKernelGGL((rms_norm_scalar_kernel<true, false>), grid, dim3(256), 0, s, a);
+  else if (a.weight_fp32) hipLaunchKernelGGL((rms_norm_scalar_kernel<false, true>), grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((rms_norm_scalar_kernel<false, false>), grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t silu_mul(const SiluArgs& a, hipStream_t s) {
+  const uint16_t* gu = reinterpret_cast<const uint16_t*>(a.gate_up);
+  uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
+  if ((a.rows * a.d + 255) / 256 > 0x7fffffff) return hipErrorInvalidValue;
+  if (a.vec_ok) {
+    const int d_chunks = a.d / 8;
+    const int64_t total = a.rows * d_chunks;
+    hipLaunchKernelGGL(silu_mul_vec_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, gu, out, total,
+                       d_chunks);
+  } else {
+    const int64_t total = a.rows * a.d;
+    hipLaunchKernelGGL(silu_mul_scalar_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, gu, out,
+                       total, a.d);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace bvllm

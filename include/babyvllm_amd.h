@@ -37,7 +37,7 @@ extern "C" {
 #endif
 
 /* ABI version of this header; bumped on any signature change. */
-#define BVLLM_ABI_VERSION 3
+#define BVLLM_ABI_VERSION 4
 
 #if defined(__GNUC__)
 #define BVLLM_API __attribute__((visibility("default")))
@@ -137,6 +137,37 @@ BVLLM_API int bvllm_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_s
                         int32_t single_query_seqs,
                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                         int32_t block_size, void* stream);
+
+/*
+ * Greedy sampling: out[r] = argmax(logits[r, :]) for rows r < rows. Replaces
+ * greedy_argmax (babyvllm/kernels/argmax.py:41-56) and its two kernels
+ * (argmax.py:14-38). logits [rows, vocab] with unit column stride and row
+ * stride row_stride elements, bf16 (logits_fp32 = 0) or fp32 (1); out int64.
+ * Ties go to the lowest index and NaN beats every number, as torch.argmax.
+ * `workspace` must hold bvllm_argmax_workspace_bytes(rows, vocab) bytes.
+ */
+BVLLM_API int64_t bvllm_argmax_workspace_bytes(int32_t rows, int32_t vocab);
+BVLLM_API int bvllm_greedy_argmax(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                        int32_t logits_fp32, void* workspace, int64_t* out, void* stream);
+
+/*
+ * Residual add + RMSNorm over rows of `hidden` bf16 elements. Replaces
+ * fused_add_rms_norm (babyvllm/kernels/layernorm.py:46-83, kernel :5-43).
+ * If residual is non-NULL: x = bf16(input + residual), written back to
+ * residual; else x = input. out = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w),
+ * weight [hidden] bf16 (weight_fp32 = 0) or fp32 (1). Strides in elements.
+ */
+BVLLM_API int bvllm_fused_add_rms_norm(const void* input, int64_t input_stride, void* residual,
+                             int64_t residual_stride, const void* weight, int32_t weight_fp32,
+                             void* out, int64_t out_stride, int32_t rows, int32_t hidden, float eps,
+                             void* stream);
+
+/*
+ * out[r, c] = bf16(silu(gate_up[r, c]) * gate_up[r, d + c]), silu in fp32.
+ * Replaces fused_silu_mul (babyvllm/kernels/activation.py:44-65, kernel :5-42).
+ * gate_up [rows, 2d] and out [rows, d] bf16, contiguous.
+ */
+BVLLM_API int bvllm_silu_mul(const void* gate_up, int64_t rows, int32_t d, void* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -12,6 +12,10 @@ path for the three hot-path operations:
 * Varlen paged prefill attention: ``_paged_attention_torch`` + ``_causal_sdpa``
   (attention.py:137-196).
 
+* The decode step's other kernels (the next row of the path): greedy argmax,
+  residual add + RMSNorm and SiLU·mul (``decode_step.py``; the reference's
+  Triton kernel math, babyvllm/kernels/argmax.py, layernorm.py, activation.py).
+
 It also holds independent float64 brute-force restatements used to pin the
 torch restatement (see tests/test_oracle.py).
 
@@ -23,5 +27,7 @@ Parity status per function (pins live in tests/test_oracle.py):
   rope_tables, apply_rope, apply_rope_bf16_explicit, store_kvcache,
   gather_kv_batched, make_decode_mask, static_decode_attention,
   paged_attention_torch, causal_sdpa, naive_causal_attention,
-  brute_decode, brute_prefill, lse_merge            -- all pinned.
+  brute_decode, brute_prefill, lse_merge,
+  decode_step.greedy_argmax, decode_step.fused_add_rms_norm,
+  decode_step.silu_mul                             -- all pinned.
 """

@@ -1,0 +1,203 @@
+"""The decode step's other kernels on the GPU: greedy argmax, residual add +
+RMSNorm and SiLU·mul (ports tests/test_argmax_kernel.py and covers
+babyvllm/kernels/layernorm.py, activation.py).
+
+Oracle: oracle/decode_step.py on the CPU. Argmax and the residual update are
+bit-exact; normalised and activated outputs are within one bf16 ulp of the
+oracle (the fp32 sums of squares and exp differ from torch's in the last bits,
+which moves a value across a bf16 rounding boundary only rarely).
+"""
+
+import pytest
+import torch
+
+from oracle import decode_step as ds
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a ROCm GPU"),
+]
+
+
+def _argmax():
+    from babyvllm.kernels.argmax import greedy_argmax
+    return greedy_argmax
+
+
+def _ulps(a, b):
+    """Distance in bf16 ulps of two bf16 tensors (same sign assumed near equality)."""
+    ai = a.view(torch.int16).to(torch.int32)
+    bi = b.view(torch.int16).to(torch.int32)
+    ai = torch.where(ai < 0, -32768 - ai, ai)
+    bi = torch.where(bi < 0, -32768 - bi, bi)
+    return (ai - bi).abs()
+
+
+# --------------------------------------------------------------------- argmax
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("rows,vocab", [(1, 151936), (64, 152064), (7, 4097), (3, 100)])
+def test_matches_torch_argmax(rows, vocab, dtype):
+    g = torch.Generator(device="cuda").manual_seed(rows + vocab)
+    x = torch.randn(rows, vocab, device="cuda", dtype=dtype, generator=g) * 4
+    out = torch.empty(rows, dtype=torch.int64, device="cuda")
+    _argmax()(x, out)
+    assert torch.equal(out, x.argmax(-1))
+    assert torch.equal(out.cpu(), ds.greedy_argmax(x.cpu()))
+
+
+def test_ties_go_to_the_lowest_index_across_chunks():
+    vocab = 20000
+    x = torch.zeros(6, vocab, device="cuda", dtype=torch.bfloat16)
+    x[0, [5, 9000, 19999]] = 3.0            # first chunk wins
+    x[1, [8191, 8192]] = 3.0                # straddles the kernel's chunk boundary
+    x[2, [12000, 8200]] = 3.0               # later chunk listed first
+    x[3, 19999] = 3.0                       # last, partial chunk
+    x[5, [4095, 4096]] = 3.0                # straddles the reference's block boundary
+    # row 4 all equal: index 0
+    out = torch.empty(6, dtype=torch.int64, device="cuda")
+    _argmax()(x, out, block=4096)
+    assert out.tolist() == [5, 8191, 8200, 19999, 0, 4095]
+    assert torch.equal(out, x.argmax(-1))
+
+
+def test_row_slice_of_a_larger_buffer():
+    buf = torch.randn(64, 152064, device="cuda", dtype=torch.bfloat16)
+    out = torch.full((64,), -1, dtype=torch.int64, device="cuda")
+    _argmax()(buf[:5], out[:5])
+    assert torch.equal(out[:5], buf[:5].argmax(-1))
+    assert (out[5:] == -1).all()
+
+
+def test_column_slice_and_unaligned_rows():
+    buf = torch.randn(9, 5003, device="cuda", dtype=torch.bfloat16)
+    view = buf[:, 1:5001]                    # row stride 5003, unaligned start
+    out = torch.empty(9, dtype=torch.int64, device="cuda")
+    _argmax()(view, out)
+    assert torch.equal(out, view.argmax(-1))
+
+
+def test_nan_is_the_maximum_and_the_first_nan_wins():
+    x = torch.randn(3, 9000, device="cuda", dtype=torch.float32)
+    x[0, [8500, 17]] = float("nan")
+    x[1, 8999] = float("nan")
+    out = torch.empty(3, dtype=torch.int64, device="cuda")
+    _argmax()(x, out)
+    assert out.tolist()[:2] == [17, 8999]
+    assert torch.equal(out.cpu(), ds.greedy_argmax(x.cpu()))
+
+
+# -------------------------------------------------------------------- RMSNorm
+
+def _rms():
+    from babyvllm.kernels.layernorm import fused_add_rms_norm
+    return fused_add_rms_norm
+
+
+@pytest.mark.parametrize("rows,hidden", [(64, 3584), (1024, 3584), (7, 896), (3, 100), (5, 4104), (2, 20000)])
+@pytest.mark.parametrize("with_residual", [True, False])
+@pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32])
+def test_rms_norm_matches_oracle(rows, hidden, with_residual, wdtype):
+    g = torch.Generator(device="cuda").manual_seed(rows * 7 + hidden)
+    x = (torch.randn(rows, hidden, device="cuda", generator=g) * 2).to(torch.bfloat16)
+    res = torch.randn(rows, hidden, device="cuda", generator=g).to(torch.bfloat16) if with_residual else None
+    w = (torch.rand(hidden, device="cuda", generator=g) + 0.5).to(wdtype)
+    eps = 1e-6
+    exp_out, exp_res = ds.fused_add_rms_norm(x.cpu(), None if res is None else res.cpu(), w.cpu(), eps)
+    x_before = x.clone()
+    out = _rms()(x, res, w, eps)
+    assert out.shape == x.shape and out.dtype == torch.bfloat16
+    if with_residual:
+        assert torch.equal(res.cpu(), exp_res)
+    assert torch.equal(x, x_before)
+    d = _ulps(out.cpu(), exp_out)
+    assert int(d.max()) <= 1
+    assert float((d > 0).float().mean()) < 1e-3
+
+
+def test_rms_norm_of_a_strided_view_and_3d_input():
+    big = torch.randn(6, 4000, device="cuda").to(torch.bfloat16)
+    view = big[:, :3584]
+    w = torch.ones(3584, device="cuda", dtype=torch.bfloat16)
+    out = _rms()(view, None, w, 1e-6)
+    exp, _ = ds.fused_add_rms_norm(view.cpu(), None, w.cpu(), 1e-6)
+    assert int(_ulps(out.cpu(), exp).max()) <= 1
+    x3 = torch.randn(2, 3, 896, device="cuda").to(torch.bfloat16)
+    r3 = torch.randn(2, 3, 896, device="cuda").to(torch.bfloat16)
+    w3 = torch.rand(896, device="cuda", dtype=torch.float32)
+    e3, er3 = ds.fused_add_rms_norm(x3.cpu(), r3.cpu(), w3.cpu(), 1e-5)
+    o3 = _rms()(x3, r3, w3, 1e-5)
+    assert o3.shape == (2, 3, 896) and torch.equal(r3.cpu(), er3)
+    assert int(_ulps(o3.cpu(), e3).max()) <= 1
+
+
+def test_rms_norm_refuses_a_non_viewable_residual():
+    x = torch.randn(4, 64, device="cuda").to(torch.bfloat16)
+    res = torch.randn(64, 4, device="cuda").to(torch.bfloat16).t()
+    with pytest.raises(AssertionError):
+        _rms()(x, res, torch.ones(64, device="cuda", dtype=torch.bfloat16), 1e-6)
+
+
+# ------------------------------------------------------------------- SiLU·mul
+
+def _silu():
+    from babyvllm.kernels.activation import fused_silu_mul
+    return fused_silu_mul
+
+
+@pytest.mark.parametrize("shape", [(64, 2 * 18944), (8192, 2 * 1024), (7, 2 * 100), (2, 5, 2 * 64)])
+def test_silu_mul_matches_oracle(shape):
+    g = torch.Generator(device="cuda").manual_seed(sum(shape))
+    gu = (torch.randn(*shape, device="cuda", generator=g) * 3).to(torch.bfloat16)
+    out = _silu()(gu)
+    exp = ds.silu_mul(gu.cpu())
+    assert out.shape == exp.shape
+    d = _ulps(out.cpu(), exp)
+    assert int(d.max()) <= 1
+    assert float((d > 0).float().mean()) < 1e-3
+
+
+# ------------------------------------------------------------- in a hip graph
+
+def test_decode_step_tail_replays_in_a_hip_graph():
+    """norm -> (stand-in LM head) -> argmax, and SiLU·mul, captured once and
+    replayed with new inputs: every replay equals the eager result."""
+    rows, hidden, vocab = 64, 896, 5000
+    x = torch.randn(rows, hidden, device="cuda").to(torch.bfloat16)
+    res = torch.randn(rows, hidden, device="cuda").to(torch.bfloat16)
+    w = torch.rand(hidden, device="cuda").to(torch.bfloat16)
+    head = (torch.randn(vocab, hidden, device="cuda") * 0.05).to(torch.bfloat16)
+    gu = torch.randn(rows, 2 * 256, device="cuda").to(torch.bfloat16)
+    tokens = torch.empty(rows, dtype=torch.int64, device="cuda")
+
+    def step():
+        h = _rms()(x, res, w, 1e-6)
+        logits = h @ head.t().contiguous()
+        _argmax()(logits, tokens)
+        return _silu()(gu), logits
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    res0 = res.clone()
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    res.copy_(res0)
+    with torch.cuda.graph(graph):
+        act, logits = step()
+    for seed in range(3):
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        x.copy_(torch.randn(rows, hidden, device="cuda", generator=g).to(torch.bfloat16))
+        res.copy_(res0)
+        gu.copy_(torch.randn(rows, 2 * 256, device="cuda", generator=g).to(torch.bfloat16))
+        graph.replay()
+        torch.cuda.synchronize()
+        g_tokens, g_act, g_res = tokens.clone(), act.clone(), res.clone()
+        res.copy_(res0)
+        e_act, e_logits = step()
+        torch.cuda.synchronize()
+        assert torch.equal(g_act, e_act)
+        assert torch.equal(g_res, res)
+        assert torch.equal(g_tokens, tokens)
+        assert torch.equal(tokens, e_logits.argmax(-1))
