@@ -17,7 +17,7 @@ namespace bvllm {
 namespace {
 
 constexpr int kArgmaxThreads = 256;
-constexpr int kChunk = 8192;  // columns per stage-1 work-group
+constexpr int kChunk = 4096;  // columns per stage-1 work-group
 
 struct Best {
   float v;
@@ -83,18 +83,45 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_chunks_kernel(const T* 
   const int hi = min(lo + kChunk, vocab);
   Best b{-__builtin_huge_valf(), 0x7fffffff};
   if (ALIGNED) {
-    // Each thread walks its 16-byte vectors in increasing column order.
-    for (int c = lo + threadIdx.x * VEC; c < hi; c += kArgmaxThreads * VEC) {
-      const uint4 raw = ld16(x + c);
-      const T* e = reinterpret_cast<const T*>(&raw);
+    // All of a thread's 16-byte vectors are requested before the first is
+    // used. The thread's maximum is taken with plain max operations (and a
+    // NaN flag), then its first column holding that maximum (or its first
+    // NaN) is found: fewer operations per element than a running comparison.
+    constexpr int PER = kChunk / (kArgmaxThreads * VEC);
+    uint4 raw[PER];
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) {
-        const float v = to_f32<T>(e[k]);
-        if (c + k < hi && better(v, c + k, b.v, b.i)) {
-          b.v = v;
-          b.i = c + k;
-        }
+    for (int k = 0; k < PER; ++k) {
+      const int c = lo + (threadIdx.x + k * kArgmaxThreads) * VEC;
+      raw[k] = c < hi ? ld16(x + c) : make_uint4(0, 0, 0, 0);
+    }
+    float m = -__builtin_huge_valf();
+    bool any_nan = false;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int c = lo + (threadIdx.x + k * kArgmaxThreads) * VEC;
+      const T* e = reinterpret_cast<const T*>(&raw[k]);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const float v = c + j < hi ? to_f32<T>(e[j]) : -__builtin_huge_valf();
+        m = fmaxf(m, v);
+        any_nan |= v != v;
       }
+    }
+    int first = 0x7fffffff;
+#pragma unroll
+    for (int k = PER - 1; k >= 0; --k) {
+      const int c = lo + (threadIdx.x + k * kArgmaxThreads) * VEC;
+      const T* e = reinterpret_cast<const T*>(&raw[k]);
+#pragma unroll
+      for (int j = VEC - 1; j >= 0; --j) {
+        const float v = to_f32<T>(e[j]);
+        const bool hit = c + j < hi && (any_nan ? v != v : v == m);
+        first = hit ? c + j : first;
+      }
+    }
+    if (first != 0x7fffffff) {
+      b.v = any_nan ? __builtin_nanf("") : m;
+      b.i = first;
     }
   } else {
     for (int c = lo + threadIdx.x; c < hi; c += kArgmaxThreads) {

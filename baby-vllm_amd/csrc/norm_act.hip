@@ -38,9 +38,11 @@ __device__ __forceinline__ float weight_at(const void* w, int i) {
 }
 
 // CPL: 16-byte chunks (8 bf16) per lane; the row has n ≤ 64·CPL·8 elements.
-template <int CPL, bool HAS_RES, bool W32>
-__global__ __launch_bounds__(256) void rms_norm_vec_kernel(NormArgs a) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+// RPW rows per work-group, one wave each (RPW = 1 spreads a short batch over
+// as many compute units as it has rows).
+template <int CPL, bool HAS_RES, bool W32, int RPW>
+__global__ __launch_bounds__(64 * RPW) void rms_norm_vec_kernel(NormArgs a) {
+  const int row = blockIdx.x * RPW + (threadIdx.x >> 6);
   if (row >= a.rows) return;
   const int lane = threadIdx.x & 63;
   const int chunks = a.n / 8;
@@ -48,13 +50,23 @@ __global__ __launch_bounds__(256) void rms_norm_vec_kernel(NormArgs a) {
   uint16_t* res = reinterpret_cast<uint16_t*>(a.residual) + (int64_t)row * a.res_stride;
   uint16_t* out = reinterpret_cast<uint16_t*>(a.out) + (int64_t)row * a.out_stride;
 
+  // Row, residual and weight are all requested before the first use (one
+  // memory round trip per row).
   uint4 xv[CPL];
   uint4 rv[CPL];
+  uint4 wv[CPL][W32 ? 2 : 1];
 #pragma unroll
   for (int k = 0; k < CPL; ++k) {
     const int c = lane + 64 * k;
     xv[k] = c < chunks ? ld16(in + 8 * c) : make_uint4(0, 0, 0, 0);
     if (HAS_RES) rv[k] = c < chunks ? ld16(res + 8 * c) : make_uint4(0, 0, 0, 0);
+    if constexpr (W32) {
+      const float* wp = reinterpret_cast<const float*>(a.weight) + 8 * c;
+      wv[k][0] = c < chunks ? ld16(wp) : make_uint4(0, 0, 0, 0);
+      wv[k][1] = c < chunks ? ld16(wp + 4) : make_uint4(0, 0, 0, 0);
+    } else {
+      wv[k][0] = c < chunks ? ld16(reinterpret_cast<const uint16_t*>(a.weight) + 8 * c) : make_uint4(0, 0, 0, 0);
+    }
   }
   float ss = 0.f;
 #pragma unroll
@@ -84,18 +96,15 @@ __global__ __launch_bounds__(256) void rms_norm_vec_kernel(NormArgs a) {
     const uint32_t* xw = reinterpret_cast<const uint32_t*>(&xv[k]);
     float w[8];
     if constexpr (W32) {
-      const float* wp = reinterpret_cast<const float*>(a.weight) + 8 * c;
-      const uint4 w0 = ld16(wp), w1 = ld16(wp + 4);
-      const float* f0 = reinterpret_cast<const float*>(&w0);
-      const float* f1 = reinterpret_cast<const float*>(&w1);
+      const float* f0 = reinterpret_cast<const float*>(&wv[k][0]);
+      const float* f1 = reinterpret_cast<const float*>(&wv[k][W32 ? 1 : 0]);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         w[q] = f0[q];
         w[4 + q] = f1[q];
       }
     } else {
-      const uint4 wv = ld16(reinterpret_cast<const uint16_t*>(a.weight) + 8 * c);
-      const uint32_t* ww = reinterpret_cast<const uint32_t*>(&wv);
+      const uint32_t* ww = reinterpret_cast<const uint32_t*>(&wv[k][0]);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         w[2 * q] = lo_f32(ww[q]);
@@ -136,14 +145,20 @@ __global__ __launch_bounds__(256) void rms_norm_scalar_kernel(NormArgs a) {
   for (int i = lane; i < a.n; i += 64) out[i] = norm_out(bf16_to_f32(src[i]), r, weight_at<W32>(a.weight, i));
 }
 
-template <int CPL>
-hipError_t launch_norm_vec(const NormArgs& a, dim3 grid, hipStream_t s) {
+template <int CPL, int RPW>
+hipError_t launch_norm_vec_rpw(const NormArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)((a.rows + RPW - 1) / RPW)), block(64 * RPW);
   const bool res = a.residual != nullptr;
-  if (res && a.weight_fp32) hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, true, true>), grid, dim3(256), 0, s, a);
-  else if (res) hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, true, false>), grid, dim3(256), 0, s, a);
-  else if (a.weight_fp32) hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, false, true>), grid, dim3(256), 0, s, a);
-  else hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, false, false>), grid, dim3(256), 0, s, a);
+  if (res && a.weight_fp32) hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, true, true, RPW>), grid, block, 0, s, a);
+  else if (res) hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, true, false, RPW>), grid, block, 0, s, a);
+  else if (a.weight_fp32) hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, false, true, RPW>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, false, false, RPW>), grid, block, 0, s, a);
   return hipGetLastError();
+}
+
+template <int CPL>
+hipError_t launch_norm_vec(const NormArgs& a, hipStream_t s) {
+  return a.rows >= 1024 ? launch_norm_vec_rpw<CPL, 4>(a, s) : launch_norm_vec_rpw<CPL, 1>(a, s);
 }
 
 // Vector form: 8 gate and 8 up elements per thread.
@@ -186,10 +201,10 @@ hipError_t fused_add_rms_norm(const NormArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)((a.rows + 3) / 4));
   if (a.vec_ok) {
     const int chunks = a.n / 8;
-    if (chunks <= 64 * 2) return launch_norm_vec<2>(a, grid, s);
-    if (chunks <= 64 * 4) return launch_norm_vec<4>(a, grid, s);
-    if (chunks <= 64 * 8) return launch_norm_vec<8>(a, grid, s);
-    if (chunks <= 64 * 16) return launch_norm_vec<16>(a, grid, s);
+    if (chunks <= 64 * 2) return launch_norm_vec<2>(a, s);
+    if (chunks <= 64 * 4) return launch_norm_vec<4>(a, s);
+    if (chunks <= 64 * 8) return launch_norm_vec<8>(a, s);
+    if (chunks <= 64 * 16) return launch_norm_vec<16>(a, s);
   }
   const bool res = a.residual != nullptr;
   if (res && a.weight_fp32) hipLaunchKernelGGL((rms_norm_scalar_kernel<true, true>), grid, dim3(256), 0, s, a);

@@ -18,7 +18,9 @@ Infinity Cache), exactly the reference's method (benchmarks/bench_decode_attn.py
 
 Secondary lines (same method): decode B8/ctx1920, B1/ctx32768, B64/ctx2048 (the
 reference's published H100 point), RoPE + KV append (decode 64 tokens, prefill
-8192 tokens), and the four varlen prefill configurations in TFLOP/s.
+8192 tokens), the four varlen prefill configurations in TFLOP/s, and the decode
+step's other kernels (greedy argmax over 64 x 152,064 logits, residual add +
+RMSNorm and SiLU*mul at 64 and 8192 rows) in GB/s.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
                        [--only NAME] [--calib-copy]
@@ -234,6 +236,47 @@ def bench_prefill(name, warmup, iters, layers=LAYERS):
             "frac_of_bf16_peak": flops / (per_us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, "flop": flops}
 
 
+def bench_step_kernels(warmup, iters):
+    """The decode step's other kernels at the 7B shape, each over enough distinct
+    buffers per replay that the inputs come from HBM (argmax, prefill-size rows)
+    or as the decode step meets them (decode-size rows are cache-resident)."""
+    from babyvllm.kernels.activation import fused_silu_mul
+    from babyvllm.kernels.argmax import greedy_argmax
+    from babyvllm.kernels.layernorm import fused_add_rms_norm
+
+    hidden, inter, vocab = 3584, 18944, 152064
+    out = {}
+
+    def line(name, per_us, nbytes, reps):
+        out[name] = {"us_per_call": per_us, "gb_s": nbytes / (per_us * 1e-6) / 1e9,
+                     "frac_of_hbm_peak": nbytes / (per_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                     "algorithmic_bytes": nbytes, "calls_per_replay": reps}
+
+    g = torch.Generator(device="cuda").manual_seed(11)
+    reps = 16
+    logits = [torch.randn(64, vocab, device="cuda", dtype=torch.bfloat16, generator=g) for _ in range(reps)]
+    tok = torch.empty(64, dtype=torch.int64, device="cuda")
+    ms, _ = time_graph(lambda: [greedy_argmax(x, tok) for x in logits], warmup, iters)
+    line("argmax_64x152064_bf16", ms * 1e3 / reps, 64 * vocab * 2, reps)
+    del logits
+
+    w = torch.rand(hidden, device="cuda", generator=g).to(torch.bfloat16)
+    for rows, reps in ((64, 56), (8192, 8)):
+        xs = [torch.randn(rows, hidden, device="cuda", generator=g).to(torch.bfloat16) for _ in range(reps)]
+        rs = [torch.randn(rows, hidden, device="cuda", generator=g).to(torch.bfloat16) for _ in range(reps)]
+        ms, _ = time_graph(lambda: [fused_add_rms_norm(x, r, w, 1e-6) for x, r in zip(xs, rs)], warmup, iters)
+        line(f"add_rms_norm_{rows}x{hidden}", ms * 1e3 / reps, rows * hidden * 2 * 4 + hidden * 2, reps)
+        del xs, rs
+
+    for rows, reps in ((64, 28), (8192, 2)):
+        gus = [torch.randn(rows, 2 * inter, device="cuda", generator=g).to(torch.bfloat16) for _ in range(reps)]
+        ms, _ = time_graph(lambda: [fused_silu_mul(x) for x in gus], warmup, iters)
+        line(f"silu_mul_{rows}x{inter}", ms * 1e3 / reps, rows * inter * 2 * 3, reps)
+        del gus
+    torch.cuda.empty_cache()
+    return out
+
+
 # ------------------------------------------------------------ CPU baseline
 
 def cpu_baseline(batch, ctx, budget_s=15.0):
@@ -302,7 +345,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary lines")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None,
-                    help="decode_b64 | decode_b8 | decode_b1 | append | prefill | prefill:<shape>")
+                    help="decode_b64 | decode_b8 | decode_b1 | append | prefill | prefill:<shape> | step")
     ap.add_argument("--calib-copy", action="store_true")
     args = ap.parse_args()
 
@@ -339,6 +382,9 @@ def main():
         print(json.dumps({n: bench_prefill(n, args.warmup, args.steps) for n in PREFILL_SHAPES}),
               flush=True)
         return
+    if args.only == "step":
+        print(json.dumps(bench_step_kernels(args.warmup, args.steps)), flush=True)
+        return
     if args.only and args.only.startswith("prefill:"):
         name = args.only.split(":", 1)[1]
         print(json.dumps({name: bench_prefill(name, args.warmup, args.steps)}), flush=True)
@@ -362,6 +408,8 @@ def main():
         for name in PREFILL_SHAPES:
             log(f"prefill {name} ...")
             secondary[f"prefill_{name}"] = bench_prefill(name, args.warmup, max(5, args.steps // 5))
+        log("decode-step kernels (argmax, add + RMSNorm, SiLU*mul) ...")
+        secondary.update(bench_step_kernels(args.warmup, max(5, args.steps // 5)))
         secondary["reference_h100_published"] = {
             "decode_b64_ctx2048_gb_s": 2514.9, "prefill_1x(2048+4096)_ms": 1.2615,
             "source": "results_28Oct2026_H100_flash_decode/decode_attn_bench.json:1200-1208; "
