@@ -25,10 +25,14 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-__device__ __forceinline__ float add_bf16(float a, float b) { return bf16_to_f32(f32_to_bf16_rne(a + b)); }
+// Round to bf16 with the hardware converter (v_cvt_pk_bf16_f32, round to
+// nearest even), as a value and as packed pairs.
+__device__ __forceinline__ float round_bf16(float x) { return lo_f32(pack_bf16x2_hw(x, 0.f)); }
+
+__device__ __forceinline__ float add_bf16(float a, float b) { return round_bf16(a + b); }
 
 __device__ __forceinline__ uint16_t norm_out(float x, float r, float w) {
-  return (uint16_t)f32_to_bf16_rne(bf16_to_f32(f32_to_bf16_rne(x * r)) * w);
+  return (uint16_t)pack_bf16x2_hw(round_bf16(x * r) * w, 0.f);
 }
 
 template <bool W32>
@@ -37,14 +41,19 @@ __device__ __forceinline__ float weight_at(const void* w, int i) {
   else return bf16_to_f32(reinterpret_cast<const uint16_t*>(w)[i]);
 }
 
-// CPL: 16-byte chunks (8 bf16) per lane; the row has n ≤ 64·CPL·8 elements.
-// RPW rows per work-group, one wave each (RPW = 1 spreads a short batch over
-// as many compute units as it has rows).
-template <int CPL, bool HAS_RES, bool W32, int RPW>
-__global__ __launch_bounds__(64 * RPW) void rms_norm_vec_kernel(NormArgs a) {
-  const int row = blockIdx.x * RPW + (threadIdx.x >> 6);
-  if (row >= a.rows) return;
-  const int lane = threadIdx.x & 63;
+// CPL: 16-byte chunks (8 bf16) per lane; the row has n ≤ 64·WPR·CPL·8
+// elements. RPW rows per work-group with WPR waves per row (one of the two is
+// 1): many rows take one wave each; a short batch (decode) splits each row
+// over 4 waves, and the waves' sums of squares meet in LDS.
+template <int CPL, bool HAS_RES, bool W32, int RPW, int WPR>
+__global__ __launch_bounds__(64 * RPW * WPR) void rms_norm_vec_kernel(NormArgs a) {
+  static_assert(RPW == 1 || WPR == 1, "rows per work-group or waves per row");
+  __shared__ float wsum[RPW * WPR];
+  const int wave = threadIdx.x >> 6;
+  const int row = blockIdx.x * RPW + (RPW > 1 ? wave : 0);
+  if (row >= a.rows) return;  // uniform over the work-group when WPR > 1
+  const int lane = WPR > 1 ? (int)threadIdx.x : (int)(threadIdx.x & 63);  // lane within the row
+  constexpr int LPR = 64 * WPR;                                             // lanes per row
   const int chunks = a.n / 8;
   const uint16_t* in = reinterpret_cast<const uint16_t*>(a.input) + (int64_t)row * a.in_stride;
   uint16_t* res = reinterpret_cast<uint16_t*>(a.residual) + (int64_t)row * a.res_stride;
@@ -57,7 +66,7 @@ __global__ __launch_bounds__(64 * RPW) void rms_norm_vec_kernel(NormArgs a) {
   uint4 wv[CPL][W32 ? 2 : 1];
 #pragma unroll
   for (int k = 0; k < CPL; ++k) {
-    const int c = lane + 64 * k;
+    const int c = lane + LPR * k;
     xv[k] = c < chunks ? ld16(in + 8 * c) : make_uint4(0, 0, 0, 0);
     if (HAS_RES) rv[k] = c < chunks ? ld16(res + 8 * c) : make_uint4(0, 0, 0, 0);
     if constexpr (W32) {
@@ -76,8 +85,8 @@ __global__ __launch_bounds__(64 * RPW) void rms_norm_vec_kernel(NormArgs a) {
       const uint32_t* rw = reinterpret_cast<const uint32_t*>(&rv[k]);
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        xw[q] = pack_bf16x2(add_bf16(lo_f32(xw[q]), lo_f32(rw[q])), add_bf16(hi_f32(xw[q]), hi_f32(rw[q])));
-      const int c = lane + 64 * k;
+        xw[q] = pack_bf16x2_hw(lo_f32(xw[q]) + lo_f32(rw[q]), hi_f32(xw[q]) + hi_f32(rw[q]));
+      const int c = lane + LPR * k;
       if (c < chunks) st16(res + 8 * c, xv[k]);
     }
 #pragma unroll
@@ -88,10 +97,17 @@ __global__ __launch_bounds__(64 * RPW) void rms_norm_vec_kernel(NormArgs a) {
     }
   }
   ss = wave_sum(ss);
+  if constexpr (WPR > 1) {
+    if ((threadIdx.x & 63) == 0) wsum[wave] = ss;
+    __syncthreads();
+    ss = 0.f;
+#pragma unroll
+    for (int w = 0; w < WPR; ++w) ss += wsum[w];
+  }
   const float r = 1.f / sqrtf(ss / (float)a.n + a.eps);
 #pragma unroll
   for (int k = 0; k < CPL; ++k) {
-    const int c = lane + 64 * k;
+    const int c = lane + LPR * k;
     if (c >= chunks) continue;
     const uint32_t* xw = reinterpret_cast<const uint32_t*>(&xv[k]);
     float w[8];
@@ -114,8 +130,10 @@ __global__ __launch_bounds__(64 * RPW) void rms_norm_vec_kernel(NormArgs a) {
     uint4 o;
     uint32_t* ow = reinterpret_cast<uint32_t*>(&o);
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      ow[q] = (uint32_t)norm_out(lo_f32(xw[q]), r, w[2 * q]) | ((uint32_t)norm_out(hi_f32(xw[q]), r, w[2 * q + 1]) << 16);
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t n2 = pack_bf16x2_hw(lo_f32(xw[q]) * r, hi_f32(xw[q]) * r);  // bf16(x·r), two at a time
+      ow[q] = pack_bf16x2_hw(lo_f32(n2) * w[2 * q], hi_f32(n2) * w[2 * q + 1]);
+    }
     st16(out + 8 * c, o);
   }
 }
@@ -145,20 +163,27 @@ __global__ __launch_bounds__(256) void rms_norm_scalar_kernel(NormArgs a) {
   for (int i = lane; i < a.n; i += 64) out[i] = norm_out(bf16_to_f32(src[i]), r, weight_at<W32>(a.weight, i));
 }
 
-template <int CPL, int RPW>
-hipError_t launch_norm_vec_rpw(const NormArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)((a.rows + RPW - 1) / RPW)), block(64 * RPW);
+template <int CPL, int RPW, int WPR>
+hipError_t launch_norm_vec_shape(const NormArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)((a.rows + RPW - 1) / RPW)), block(64 * RPW * WPR);
   const bool res = a.residual != nullptr;
-  if (res && a.weight_fp32) hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, true, true, RPW>), grid, block, 0, s, a);
-  else if (res) hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, true, false, RPW>), grid, block, 0, s, a);
-  else if (a.weight_fp32) hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, false, true, RPW>), grid, block, 0, s, a);
-  else hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, false, false, RPW>), grid, block, 0, s, a);
+  if (res && a.weight_fp32)
+    hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, true, true, RPW, WPR>), grid, block, 0, s, a);
+  else if (res)
+    hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, true, false, RPW, WPR>), grid, block, 0, s, a);
+  else if (a.weight_fp32)
+    hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, false, true, RPW, WPR>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((rms_norm_vec_kernel<CPL, false, false, RPW, WPR>), grid, block, 0, s, a);
   return hipGetLastError();
 }
 
+// CPL is sized for one wave per row; with 4 waves per row each lane takes a
+// quarter (rounded up).
 template <int CPL>
 hipError_t launch_norm_vec(const NormArgs& a, hipStream_t s) {
-  return a.rows >= 1024 ? launch_norm_vec_rpw<CPL, 4>(a, s) : launch_norm_vec_rpw<CPL, 1>(a, s);
+  if (a.rows >= 1024) return launch_norm_vec_shape<CPL, 4, 1>(a, s);
+  return launch_norm_vec_shape<(CPL + 3) / 4, 1, 4>(a, s);
 }
 
 // Vector form: 8 gate and 8 up elements per thread.
@@ -179,7 +204,7 @@ __global__ __launch_bounds__(256) void silu_mul_vec_kernel(const uint16_t* __res
   for (int q = 0; q < 4; ++q) {
     const float g0 = lo_f32(gw[q]), g1 = hi_f32(gw[q]);
     const float s0 = g0 * (1.f / (1.f + expf(-g0))), s1 = g1 * (1.f / (1.f + expf(-g1)));
-    ow[q] = pack_bf16x2(s0 * lo_f32(uw[q]), s1 * hi_f32(uw[q]));
+    ow[q] = pack_bf16x2_hw(s0 * lo_f32(uw[q]), s1 * hi_f32(uw[q]));
   }
   st16(out + row * (int64_t)d_chunks * 8 + 8 * c, o);
 }
