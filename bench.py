@@ -277,6 +277,70 @@ def bench_step_kernels(warmup, iters):
     return out
 
 
+def bench_generate(n_prompts=64, prompt_len=1920, shared_len=1536, new_tokens=64, seed=0, caching=True):
+    """continuous-batching greedy generate on a random-init
+    Qwen2.5-7B-architecture model through LLM.generate's engine, prefix caching
+    on. One untimed pass captures the decode graphs; the timed pass starts from
+    an empty KV pool. Reports new tokens/s (prefill included), mean / max time
+    to first token, decode steps/s and the peak number of KV pages in use."""
+    from babyvllm.config import CacheConfig, SchedulerConfig, qwen2_5_7b
+    from babyvllm.llm import LLM
+    from babyvllm.sequence import SamplingParams
+
+    cfg = qwen2_5_7b()
+    g = torch.Generator().manual_seed(seed)
+    shared = torch.randint(0, cfg.vocab_size, (shared_len,), generator=g).tolist()
+    prompts = [shared + torch.randint(0, cfg.vocab_size, (prompt_len - shared_len,), generator=g).tolist()
+               for _ in range(n_prompts)]
+    t0 = time.perf_counter()
+    llm = LLM(cfg, cache_config=CacheConfig(num_gpu_blocks=9000, enable_prefix_caching=caching),
+              scheduler_config=SchedulerConfig(max_num_seqs=64, max_num_batched_tokens=8192), seed=seed)
+    build_s = time.perf_counter() - t0
+    params = SamplingParams(temperature=0.0, max_tokens=new_tokens, ignore_eos=True)
+    engine = llm.engine
+
+    def run():
+        engine.reset()
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for p in prompts:
+            engine.add_request(p, params)
+        first, steps, decode_steps, peak_pages, n_tokens = {}, 0, 0, 0, 0
+        while engine.has_unfinished_requests():
+            sched_running = len(engine.scheduler.running)
+            outs = engine.step()
+            now = time.perf_counter() - start
+            steps += 1
+            peak_pages = max(peak_pages, len(engine.kv_cache_manager.used_block_ids))
+            for o in outs:
+                n_tokens += len(o.new_token_ids)
+                if o.new_token_ids and o.seq_id not in first:
+                    first[o.seq_id] = now
+            if sched_running == len(engine.scheduler.running) and len(outs) == sched_running:
+                decode_steps += 1
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - start
+        return wall, first, steps, peak_pages, n_tokens, engine.kv_cache_manager.num_hit_tokens
+
+    log("  e2e warm-up pass (graph capture) ...")
+    run()
+    wall, first, steps, peak_pages, n_tokens, hits = run()
+    ttft = sorted(first.values())
+    return {
+        "metric": "end-to-end greedy generate, new tokens/s (prefill included)",
+        "tokens_per_s": n_tokens / wall, "wall_s": wall, "new_tokens": n_tokens, "engine_steps": steps,
+        "ttft_mean_ms": 1e3 * sum(ttft) / len(ttft), "ttft_max_ms": 1e3 * ttft[-1],
+        "kv_blocks_peak": peak_pages,
+        # Pages if all prompts ran at once: the shared prefix once, each private tail once.
+        "kv_blocks_closed_form_all_at_once": (shared_len // 16 + n_prompts * (-(-(prompt_len + new_tokens) // 16)
+                                                                      - shared_len // 16)),
+        "prefix_hit_tokens": hits, "model_build_s": build_s,
+        "config": {"model": "Qwen2.5-7B architecture, random init N(0, 0.02), bf16", "prompts": n_prompts,
+                   "prompt_len": prompt_len, "shared_prefix": shared_len, "new_tokens": new_tokens,
+                   "max_num_seqs": 64, "max_num_batched_tokens": 8192, "prefix_caching": caching},
+    }
+
+
 # ------------------------------------------------------------ CPU baseline
 
 def cpu_baseline(batch, ctx, budget_s=15.0):
@@ -345,7 +409,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary lines")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None,
-                    help="decode_b64 | decode_b8 | decode_b1 | append | prefill | prefill:<shape> | step")
+                    help="decode_b64 | decode_b8 | decode_b1 | append | prefill | prefill:<shape> | step | e2e")
     ap.add_argument("--calib-copy", action="store_true")
     args = ap.parse_args()
 
@@ -382,6 +446,10 @@ def main():
         print(json.dumps({n: bench_prefill(n, args.warmup, args.steps) for n in PREFILL_SHAPES}),
               flush=True)
         return
+    if args.only == "e2e":
+        print(json.dumps({"shared_prefix_caching_on": bench_generate(),
+                          "distinct_caching_off": bench_generate(shared_len=0, caching=False)}), flush=True)
+        return
     if args.only == "step":
         print(json.dumps(bench_step_kernels(args.warmup, args.steps)), flush=True)
         return
@@ -410,9 +478,14 @@ def main():
             secondary[f"prefill_{name}"] = bench_prefill(name, args.warmup, max(5, args.steps // 5))
         log("decode-step kernels (argmax, add + RMSNorm, SiLU*mul) ...")
         secondary.update(bench_step_kernels(args.warmup, max(5, args.steps // 5)))
+        log("end-to-end generate (config 5) ...")
+        secondary["generate_shared_prefix_caching_on"] = bench_generate()
+        secondary["generate_distinct_caching_off"] = bench_generate(shared_len=0, caching=False)
         secondary["reference_h100_published"] = {
             "decode_b64_ctx2048_gb_s": 2514.9, "prefill_1x(2048+4096)_ms": 1.2615,
+            "generate_b64_distinct_caching_off_tok_s": 1135.96, "generate_ttft_ms": 2902.94,
             "source": "results_28Oct2026_H100_flash_decode/decode_attn_bench.json:1200-1208; "
+                      "results_28Oct2026_H100_flash_decode/comparison_baby_partition_auto.json:705-707; "
                       "results_26Oct2026_H100/prefill_attn_bench_torch2.13.json:43-46",
         }
 
