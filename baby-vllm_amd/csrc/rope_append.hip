@@ -25,11 +25,13 @@ struct Chunk {
   uint16_t h[VW];
 };
 
-template <int VW>
+// NT: the data is read once per call (q, k, v rows), loaded with the
+// nontemporal hint; cos/sin rows are shared by all heads of a token.
+template <int VW, bool NT = false>
 __device__ __forceinline__ Chunk<VW> load_chunk(const uint16_t* p) {
   Chunk<VW> c;
   if constexpr (VW == 8) {
-    uint4 v = ld16(p);
+    uint4 v = NT ? ld16_nt(p) : ld16(p);
     c = __builtin_bit_cast(Chunk<VW>, v);
   } else if constexpr (VW == 4) {
     uint2 v = ld8(p);
@@ -103,8 +105,8 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeArgs a) {
                          : qp + (int64_t)t * a.q_st + (int64_t)head * a.q_sh;
     const uint16_t* cs = reinterpret_cast<const uint16_t*>(a.cos) + (int64_t)t * a.cs_st;
     const uint16_t* sn = reinterpret_cast<const uint16_t*>(a.sin) + (int64_t)t * a.sn_st;
-    Chunk<VW> x1 = load_chunk<VW>(row + c * VW);
-    Chunk<VW> x2 = load_chunk<VW>(row + HALF + c * VW);
+    Chunk<VW> x1 = load_chunk<VW, true>(row + c * VW);
+    Chunk<VW> x2 = load_chunk<VW, true>(row + HALF + c * VW);
     const Chunk<VW> c1 = load_chunk<VW>(cs + c * VW);
     const Chunk<VW> c2 = load_chunk<VW>(cs + HALF + c * VW);
     const Chunk<VW> s1 = load_chunk<VW>(sn + c * VW);
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeArgs a) {
     if (slot >= 0) {
       const uint16_t* src = vp + (int64_t)t * a.v_st + (int64_t)hv * a.v_sh;
       uint16_t* dst = reinterpret_cast<uint16_t*>(a.v_cache) + slot * a.vc_slot + (int64_t)hv * a.vc_head;
-      store_chunk<VW>(dst + c * VW, load_chunk<VW>(src + c * VW));
+      store_chunk<VW>(dst + c * VW, load_chunk<VW, true>(src + c * VW));
     }
   }
 }
