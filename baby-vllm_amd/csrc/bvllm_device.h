@@ -74,16 +74,31 @@ __device__ __forceinline__ f32x4_t mfma_16x16x16(const uint2& a, const uint2& b,
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Butterfly over the four 16-lane groups of a wave (lanes n, n+16, n+32, n+48).
+// IEEE maximum (NaN-propagating): lowers to v_maximum3_f32 chains with no
+// canonicalising of the operands, which fmaxf (maxnum) needs on every value
+// not known to be canonical. Same result as fmaxf for non-NaN operands (a NaN
+// score yields a NaN output either way: its exponent poisons the sum).
+__device__ __forceinline__ float fmax_prop(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// Butterfly over the four 16-lane groups of a wave (lanes n, n+16, n+32, n+48),
+// xor 16 then xor 32, with gfx950's permlane swaps (VALU, no LDS round trip).
+// permlane16_swap(x, x) leaves {g0, g0, g2, g2} in the first result and
+// {g1, g1, g3, g3} in the second (g = 16-lane group); permlane32_swap(x, x)
+// leaves {lo, lo} and {hi, hi} (32-lane halves). Combining the two results
+// lane by lane is the xor-16 (resp. xor-32) exchange: lane l gets x[l] op
+// x[l ^ 16] (resp. x[l ^ 32]), the same operands in some order, and fmax and
+// + are commutative, so the bits equal those of the shuffle form.
 __device__ __forceinline__ float max_across_groups(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16, 64));
-  x = fmaxf(x, __shfl_xor(x, 32, 64));
-  return x;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmax_prop(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmax_prop(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float sum_across_groups(float x) {
-  x += __shfl_xor(x, 16, 64);
-  x += __shfl_xor(x, 32, 64);
-  return x;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 __device__ __forceinline__ int wave_id() {

@@ -122,9 +122,9 @@ __device__ __forceinline__ void process_page(WaveState<D>& st, const PageRegs<D>
     live[i] = tok0 + i < tok_limit;
     sv[i] = live[i] ? s[i] * scale_log2 : kNegInf;
   }
-  float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+  float mx = fmax_prop(fmax_prop(sv[0], sv[1]), fmax_prop(sv[2], sv[3]));
   mx = max_across_groups(mx);
-  const float m_new = fmaxf(st.m, mx);
+  const float m_new = fmax_prop(st.m, mx);
   // A page with no live token leaves the state bit-identical: m_new == m,
   // alpha == 1 and p == 0. While no live token has been seen (m_new == -inf,
   // e.g. a padding page that opens a split's state) 0 stands in for the max,

@@ -205,67 +205,104 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   const uint16_t* vc = reinterpret_cast<const uint16_t*>(a.v_cache) + (int64_t)kvh * a.c_sh;
   const int32_t* bt = a.block_tables + (int64_t)s * a.bt_stride;
 
-  // The four page numbers of a key tile are fetched first, as scalar loads
-  // (constant address space, counted apart from the vector loads), and then all
-  // data loads of the tile are issued back to back.
+  // Staging. Chunk e = threadIdx.x + r·NW·64 (r < PER_T) of a 64-key tile is
+  // key e / CPR, 16-byte part e % CPR. Tiles start on page boundaries, so the
+  // chunk's byte offset inside its page is the same on every tile, and the 64
+  // chunks of one wave lie in one page: each load takes the page base as a
+  // scalar operand plus a loop-invariant offset. Page numbers are clamped into
+  // the pool, so every staging load is in bounds, keys at or past hi included;
+  // V rows of those keys are replaced by zeros before they reach LDS (unwritten
+  // slots may hold NaN, and 0·NaN would poison the PV product), K rows of those
+  // keys only reach scores that the mask replaces by -inf.
+  static_assert(16 % (64 / CPR) == 0, "a wave's staging chunks must lie in one page");
+  constexpr int PAGES_PER_TILE = KT / 16;
+  uint32_t st_off[PER_T];  // byte offset of the chunk inside its page
+  int st_pg[PER_T];        // page of the chunk within the tile (wave-uniform)
+  int st_key[PER_T];       // key of the chunk within the tile
+#pragma unroll
+  for (int r = 0; r < PER_T; ++r) {
+    const int e = threadIdx.x + r * NW * 64;
+    const int key = e / CPR;
+    const int part = e - key * CPR;
+    st_key[r] = key;
+    st_pg[r] = uniform(key >> 4);
+    st_off[r] = (uint32_t)(((int64_t)(key & 15) * a.c_st + part * 8) * 2);
+  }
+
+  // The four page numbers of a tile, as scalar loads (constant address space)
+  // issued together and consumed together: one wait for all four.
   typedef const int32_t __attribute__((address_space(4)))* ConstI32;
   const ConstI32 bts = (ConstI32)bt;
-  constexpr int PAGES_PER_TILE = KT / 16;
-  uint4 stk[PER_T], stv[PER_T];
-  auto stage_load = [&](int kt) {
-    int64_t page_off[PAGES_PER_TILE];
+  auto page_bases = [&](int kt, int64_t (&po)[PAGES_PER_TILE]) {
+    int raw[PAGES_PER_TILE];
 #pragma unroll
-    for (int pg = 0; pg < PAGES_PER_TILE; ++pg) {
-      int phys = bts[min(kt * PAGES_PER_TILE + pg, a.max_blocks - 1)];
-      phys = min(max(phys, 0), a.num_pages - 1);
-      page_off[pg] = (int64_t)phys * a.c_sb;
-    }
-    // Keep the four table loads together ahead of the data loads (the compiler
-    // would otherwise sink each into the branch that uses it, one wait apiece).
+    for (int pg = 0; pg < PAGES_PER_TILE; ++pg) raw[pg] = bts[min(kt * PAGES_PER_TILE + pg, a.max_blocks - 1)];
+    asm volatile("" ::"s"(raw[0]), "s"(raw[1]), "s"(raw[2]), "s"(raw[3]));
 #pragma unroll
-    for (int pg = 0; pg < PAGES_PER_TILE; ++pg) asm volatile("" ::"s"(page_off[pg]));
+    for (int pg = 0; pg < PAGES_PER_TILE; ++pg) po[pg] = (int64_t)min(max(raw[pg], 0), a.num_pages - 1) * a.c_sb;
+  };
+  static_assert(PAGES_PER_TILE == 4, "page_bases consumes four entries");
+
+  // Staging loads are inline-asm global loads, waited for explicitly before
+  // their registers are stored to LDS: the compiler's own waitcnt insertion
+  // would drain them at the loop header, serialising the next tile's memory
+  // latency with the current tile's compute.
+  u32x4_t stk[PER_T], stv[PER_T];
+  auto stage_issue = [&](const int64_t (&po)[PAGES_PER_TILE]) {
 #pragma unroll
     for (int r = 0; r < PER_T; ++r) {
-      const int e = threadIdx.x + r * NW * 64;
-      const int key = e / CPR;
-      const int part = e - key * CPR;
-      const int pos = kt * KT + key;
-      if (pos < hi) {
-        const int pg = key >> 4;  // selects instead of a dynamically indexed private array
-        const int64_t po = pg == 0 ? page_off[0] : pg == 1 ? page_off[1] : pg == 2 ? page_off[2] : page_off[3];
-        const int64_t off = po + (int64_t)(pos & 15) * a.c_st + part * 8;
-        stk[r] = ld16(kc + off);
-        stv[r] = ld16(vc + off);
-      } else {
-        stk[r] = make_uint4(0, 0, 0, 0);
-        stv[r] = make_uint4(0, 0, 0, 0);
-      }
+      const int64_t p = st_pg[r] == 0 ? po[0] : st_pg[r] == 1 ? po[1] : st_pg[r] == 2 ? po[2] : po[3];
+      const uint16_t* kb = kc + p;
+      const uint16_t* vb = vc + p;
+      asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(stk[r]) : "v"(st_off[r]), "s"(kb));
+      asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(stv[r]) : "v"(st_off[r]), "s"(vb));
     }
   };
-  auto stage_store = [&](int buf) {
+  // Waits for the staging loads of tile kt, zeroes its V rows at or past hi and
+  // stores the tile into LDS buffer buf.
+  auto stage_finish = [&](int kt, int buf) {
+    if constexpr (PER_T == 4)
+      asm volatile("s_waitcnt vmcnt(0)"
+                   : "+v"(stk[0]), "+v"(stk[1]), "+v"(stk[2]), "+v"(stk[3]),
+                     "+v"(stv[0]), "+v"(stv[1]), "+v"(stv[2]), "+v"(stv[3]));
+    else
+      asm volatile("s_waitcnt vmcnt(0)" : "+v"(stk[0]), "+v"(stk[1]), "+v"(stv[0]), "+v"(stv[1]));
+    static_assert(PER_T == 4 || PER_T == 2, "staging wait covers 2 or 4 chunks");
+    if (kt * KT + KT > hi) {  // the tile reaches hi (uniform)
+#pragma unroll
+      for (int r = 0; r < PER_T; ++r)
+        if (kt * KT + st_key[r] >= hi) stv[r] = u32x4_t{0u, 0u, 0u, 0u};
+    }
 #pragma unroll
     for (int r = 0; r < PER_T; ++r) {
       const int e = threadIdx.x + r * NW * 64;
-      const int key = e / CPR;
-      const int part = e - key * CPR;
-      st16(&lds_k[buf][key * PITCH + part * 8], stk[r]);
-      st16(&lds_v[buf][key * PITCH_V + part * 8], stv[r]);
+      const int part = e - st_key[r] * CPR;
+      *reinterpret_cast<u32x4_t*>(&lds_k[buf][st_key[r] * PITCH + part * 8]) = stk[r];
+      *reinterpret_cast<u32x4_t*>(&lds_v[buf][st_key[r] * PITCH_V + part * 8]) = stv[r];
     }
   };
 
+  // Last visible key of each column (its query position, at most hi - 1):
+  // on tiles that reach past a column's diagonal or past hi, key pos is masked
+  // for the column iff pos > lim.
+  int lim[QT];
+#pragma unroll
+  for (int ct = 0; ct < QT; ++ct) lim[ct] = min(qpos[ct], hi - 1);
+
+  int64_t po[PAGES_PER_TILE];
   if (n_tiles > 0) {
-    stage_load(0);
-    stage_store(0);
+    page_bases(0, po);
+    stage_issue(po);
+    stage_finish(0, 0);
   }
   __syncthreads();
 
-  // Staging runs on every iteration, also the last: tile n_tiles lies wholly at
-  // or past hi, so it issues no data load and stores zeros into the idle
-  // buffer. Branching on kt + 1 < n_tiles instead would leave the loads looking
-  // pending at the loop header, and the compiler would drain them there.
-  for (int kt = 0; kt < n_tiles; ++kt) {
-    const int buf = kt & 1;
-    stage_load(kt + 1);
+  // One key tile: stage tile kt + 1 into the idle buffer while tile kt computes.
+  // Staging runs on every tile, also the last: tile n_tiles is clamped into the
+  // pool like any other and its buffer is never read.
+  auto tile = [&](const int kt, const int buf) {
+    page_bases(kt + 1, po);
+    stage_issue(po);
 
     if (wave_live && kt * KT <= wave_hi) {
       const uint16_t* K = lds_k[buf];
@@ -299,20 +336,20 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
 #pragma unroll
           for (int i = 0; i < 4; ++i) sv[t][i] = sacc[ct][t][i];
         if (diag) {
+          // key 16t + 4g + i of the tile is masked iff 16t + i > lim - kt·KT - 4g.
+          const int rel = lim[ct] - kt * KT - 4 * g;
 #pragma unroll
           for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int pos = kt * KT + 16 * t + 4 * g + i;
-              if (pos > qpos[ct] || pos >= hi) sv[t][i] = kNegInf;
-            }
+            for (int i = 0; i < 4; ++i)
+              if (16 * t + i > rel) sv[t][i] = kNegInf;
         }
         float mx = kNegInf;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-          mx = fmaxf(mx, fmaxf(fmaxf(sv[t][0], sv[t][1]), fmaxf(sv[t][2], sv[t][3])));
+          mx = fmax_prop(mx, fmax_prop(fmax_prop(sv[t][0], sv[t][1]), fmax_prop(sv[t][2], sv[t][3])));
         mx = max_across_groups(mx);
-        const float m_new = fmaxf(m[ct], mx * a.scale_log2);
+        const float m_new = fmax_prop(m[ct], mx * a.scale_log2);
         const float alpha = fast_exp2(m[ct] - m_new);
         float p[4][4];
 #pragma unroll
@@ -347,16 +384,22 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
 #pragma unroll
         for (int c = 0; c < VD; ++c) {
           const uint2 lo = ld_tr16(V + (32 * u + trow) * PITCH_V + 16 * c + tcol);
-          const uint2 hi = ld_tr16(V + (32 * u + 16 + trow) * PITCH_V + 16 * c + tcol);
-          const uint4 va = make_uint4(lo.x, lo.y, hi.x, hi.y);
+          const uint2 hi2 = ld_tr16(V + (32 * u + 16 + trow) * PITCH_V + 16 * c + tcol);
+          const uint4 va = make_uint4(lo.x, lo.y, hi2.x, hi2.y);
 #pragma unroll
           for (int ct = 0; ct < QT; ++ct) acc[ct][c] = mfma_16x16x32(va, pb[ct][u], acc[ct][c]);
         }
       }
     }
 
-    stage_store(buf ^ 1);
+    stage_finish(kt + 1, buf ^ 1);
     __syncthreads();
+  };
+
+  // Two tiles per iteration, so that each tile's LDS buffer is a constant.
+  for (int kt = 0; kt < n_tiles; kt += 2) {
+    tile(kt, 0);
+    if (kt + 1 < n_tiles) tile(kt + 1, 1);
   }
 
 #pragma unroll
