@@ -82,8 +82,9 @@ extern "C" int64_t bvllm_decode_workspace_bytes(int32_t batch, int32_t num_heads
 }
 
 static bool cache_ok(const void* kc, const void* vc, int64_t sb, int64_t st, int64_t sh, int32_t nb) {
+  // The page stride is a 32-bit factor of the kernels' page-offset products.
   return kc && vc && nb > 0 && aligned16(kc) && aligned16(vc) && sb % 8 == 0 && st % 8 == 0 &&
-         sh % 8 == 0 && sb > 0 && st > 0 && sh > 0;
+         sh % 8 == 0 && sb > 0 && st > 0 && sh > 0 && sb <= 0x7fffffff;
 }
 
 extern "C" int bvllm_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,

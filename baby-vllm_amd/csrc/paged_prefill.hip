@@ -216,8 +216,13 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   // keys only reach scores that the mask replaces by -inf.
   static_assert(16 % (64 / CPR) == 0, "a wave's staging chunks must lie in one page");
   constexpr int PAGES_PER_TILE = KT / 16;
+  // Chunk e lies in page e / (16·CPR) = e / (2D) of the tile: page
+  // r·PG_STEP + (wave's offset), known at compile time up to the wave.
+  constexpr int PG_STEP = NW * 64 / (2 * D);
+  static_assert(PG_STEP * 2 * D == NW * 64 && PG_STEP * PER_T == PAGES_PER_TILE, "staging page layout");
+  static_assert(PG_STEP == 1 || PG_STEP == 2, "a wave's chunks of one r lie in page r·PG_STEP + (0 or 1)");
+  const int pg_wave = uniform((int)(threadIdx.x / (2 * D)));  // always 0 when PG_STEP == 1
   uint32_t st_off[PER_T];  // byte offset of the chunk inside its page
-  int st_pg[PER_T];        // page of the chunk within the tile (wave-uniform)
   int st_key[PER_T];       // key of the chunk within the tile
 #pragma unroll
   for (int r = 0; r < PER_T; ++r) {
@@ -225,21 +230,30 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
     const int key = e / CPR;
     const int part = e - key * CPR;
     st_key[r] = key;
-    st_pg[r] = uniform(key >> 4);
     st_off[r] = (uint32_t)(((int64_t)(key & 15) * a.c_st + part * 8) * 2);
   }
 
   // The four page numbers of a tile, as scalar loads (constant address space)
-  // issued together and consumed together: one wait for all four.
+  // issued together and consumed together: one wait for all four. Entries
+  // past the row's last table entry are clamped to it (only the last tiles
+  // reach there).
   typedef const int32_t __attribute__((address_space(4)))* ConstI32;
   const ConstI32 bts = (ConstI32)bt;
+  const uint32_t page_elems = (uint32_t)a.c_sb;  // < 2^31, checked on the host
   auto page_bases = [&](int kt, int64_t (&po)[PAGES_PER_TILE]) {
     int raw[PAGES_PER_TILE];
+    const int i0 = kt * PAGES_PER_TILE;
+    if (i0 + PAGES_PER_TILE <= a.max_blocks) {
 #pragma unroll
-    for (int pg = 0; pg < PAGES_PER_TILE; ++pg) raw[pg] = bts[min(kt * PAGES_PER_TILE + pg, a.max_blocks - 1)];
+      for (int pg = 0; pg < PAGES_PER_TILE; ++pg) raw[pg] = bts[i0 + pg];
+    } else {
+#pragma unroll
+      for (int pg = 0; pg < PAGES_PER_TILE; ++pg) raw[pg] = bts[min(i0 + pg, a.max_blocks - 1)];
+    }
     asm volatile("" ::"s"(raw[0]), "s"(raw[1]), "s"(raw[2]), "s"(raw[3]));
 #pragma unroll
-    for (int pg = 0; pg < PAGES_PER_TILE; ++pg) po[pg] = (int64_t)min(max(raw[pg], 0), a.num_pages - 1) * a.c_sb;
+    for (int pg = 0; pg < PAGES_PER_TILE; ++pg)
+      po[pg] = (int64_t)((uint64_t)(uint32_t)min(max(raw[pg], 0), a.num_pages - 1) * page_elems);
   };
   static_assert(PAGES_PER_TILE == 4, "page_bases consumes four entries");
 
@@ -251,7 +265,9 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   auto stage_issue = [&](const int64_t (&po)[PAGES_PER_TILE]) {
 #pragma unroll
     for (int r = 0; r < PER_T; ++r) {
-      const int64_t p = st_pg[r] == 0 ? po[0] : st_pg[r] == 1 ? po[1] : st_pg[r] == 2 ? po[2] : po[3];
+      int64_t p;
+      if constexpr (PG_STEP == 1) p = po[r];
+      else p = pg_wave ? po[PG_STEP * r + 1] : po[PG_STEP * r];
       const uint16_t* kb = kc + p;
       const uint16_t* vb = vc + p;
       asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(stk[r]) : "v"(st_off[r]), "s"(kb));
@@ -312,6 +328,10 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
       for (int ct = 0; ct < QT; ++ct)
 #pragma unroll
         for (int t = 0; t < 4; ++t) sacc[ct][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      // The MFMA runs are issued at raised wave priority: the SIMD's other wave
+      // (another work-group's, usually in its softmax) fills the VALU slots
+      // between them instead of delaying them.
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -322,6 +342,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
         }
       }
 
+      __builtin_amdgcn_s_setprio(0);
       uint4 pb[QT][2];
       // Some key of the tile may be invisible to some column: past the causal
       // diagonal of the wave's first query, or at/after hi.
@@ -379,6 +400,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
       // (the keys whose P this lane holds): two transpose reads.
       const int trow = 4 * g + (n >> 2);
       const int tcol = 4 * (n & 3);
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
 #pragma unroll
@@ -390,6 +412,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
           for (int ct = 0; ct < QT; ++ct) acc[ct][c] = mfma_16x16x32(va, pb[ct][u], acc[ct][c]);
         }
       }
+      __builtin_amdgcn_s_setprio(0);
     }
 
     stage_finish(kt + 1, buf ^ 1);
