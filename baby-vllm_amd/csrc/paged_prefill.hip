@@ -9,13 +9,19 @@
 // is staged once per work-group and shared by the whole GQA group:
 //   column n of a 16-column tile = (query n / G, head n % G), n < (16 / G)·G.
 // Each of the NW waves owns QT such column tiles; QB = NW·QT·(16/G).
-// Keys are processed in tiles of 64 (four 16-token pages) staged in LDS, double
-// buffered: the global loads of tile t+1 are in flight while tile t computes.
-//   Sᵀ[16 keys × 16 cols] = K · Qᵀ       (mfma 16x16x32, K operand from LDS)
-//   Oᵀ[D × 16 cols]      += Vᵀ · Pᵀ      (mfma 16x16x32 over 32 keys, Pᵀ from the
-//                                         Sᵀ registers, Vᵀ by LDS transpose reads)
-// Keys at or past hi = min(seq_len, ctx + last query + 1) are staged as zeros,
-// so cache slots that were never written (possibly NaN) never reach a product.
+// Keys come in tiles of 64 (four 16-token pages), moved from the cache into LDS
+// by direct global->LDS loads (no staging registers), rows XOR-swizzled instead
+// of padded. K and V each have two LDS buffers; K runs one tile ahead of V.
+// The products run on mfma 16x16x32 over halves of 32 keys:
+//   Sᵀ[16 keys × 16 cols] = K · Qᵀ       (K operand from LDS)
+//   Oᵀ[D × 16 cols]      += Vᵀ · Pᵀ      (Pᵀ from the Sᵀ registers, Vᵀ by LDS
+//                                         transpose reads)
+// software-pipelined by half: Sᵀ of the next half is computed while P of the
+// current half is formed, and the current PV product runs while the next
+// half's row max is taken, so MFMA and VALU work of one wave overlap.
+// Keys at or past hi = min(seq_len, ctx + last query + 1) are masked, and their
+// V rows are zeroed in LDS, so cache slots that were never written (possibly
+// NaN) never reach a product.
 //
 // Sequences with a single query token (the decode rows of a mixed step) are
 // instead computed by decode work-groups (paged_decode_wg.h) placed in front of
@@ -79,11 +85,8 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
                                                                   int xcd_group, int per_xcd, DecodeArgs dec,
                                                                   int n_dec_wgs) {
   constexpr int KT = 64;
-  // LDS row pitches (bf16 elements): K rows are read 16 B per lane from 16
-  // rows (a 16-byte pad spreads them over all banks); V rows are read by
-  // transpose reads, 32 B from each of 4 rows per 16 lanes (a 32-byte pad).
-  constexpr int PITCH = D + 8;
-  constexpr int PITCH_V = D + 16;
+  constexpr int RB = 2 * D;   // bytes of one key row of K or V (no padding)
+  constexpr int TB = 64 * RB;  // bytes of one 64-key K or V tile
   constexpr int KC = D / 32;
   constexpr int VD = D / 16;
   constexpr int CPR = D / 8;
@@ -92,9 +95,8 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   static_assert(PER_T * NW * 64 == CHUNKS, "tile chunks must divide evenly over the work-group");
   static_assert(KT == 64, "a key tile spans four 16-token pages");
 
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * KT * PITCH + 2 * KT * PITCH_V];
-  uint16_t (*lds_k)[KT * PITCH] = reinterpret_cast<uint16_t (*)[KT * PITCH]>(lds);
-  uint16_t (*lds_v)[KT * PITCH_V] = reinterpret_cast<uint16_t (*)[KT * PITCH_V]>(lds + 2 * KT * PITCH);
+  // K tiles in buffers 0 and 1, V tiles in buffers 2 and 3.
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[4 * TB];
   static_assert(NW == kDecodeWaves, "decode work-groups run with the prefill work-group size");
   static_assert(decode_lds_bytes<D, kDecodeWaves>(16) <= sizeof(lds), "decode work-group LDS");
 
@@ -191,47 +193,48 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
 #pragma unroll
     for (int c = 0; c < KC; ++c) asm volatile("" ::"v"(qreg[ct][c].x), "v"(qreg[ct][c].y), "v"(qreg[ct][c].z), "v"(qreg[ct][c].w));
 
-  float m[QT], l[QT];
+  float m[QT], l[QT], alpha[QT];
   f32x4_t acc[QT][VD];
 #pragma unroll
   for (int ct = 0; ct < QT; ++ct) {
     m[ct] = kNegInf;
     l[ct] = 0.f;
+    alpha[ct] = 1.f;
 #pragma unroll
     for (int c = 0; c < VD; ++c) acc[ct][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  const uint16_t* kc = reinterpret_cast<const uint16_t*>(a.k_cache) + (int64_t)kvh * a.c_sh;
-  const uint16_t* vc = reinterpret_cast<const uint16_t*>(a.v_cache) + (int64_t)kvh * a.c_sh;
+  const unsigned char* kc = reinterpret_cast<const unsigned char*>(a.k_cache) + (int64_t)kvh * a.c_sh * 2;
+  const unsigned char* vc = reinterpret_cast<const unsigned char*>(a.v_cache) + (int64_t)kvh * a.c_sh * 2;
   const int32_t* bt = a.block_tables + (int64_t)s * a.bt_stride;
 
-  // Staging. Chunk e = threadIdx.x + r·NW·64 (r < PER_T) of a 64-key tile is
-  // key e / CPR, 16-byte part e % CPR. Tiles start on page boundaries, so the
-  // chunk's byte offset inside its page is the same on every tile, and the 64
-  // chunks of one wave lie in one page: each load takes the page base as a
-  // scalar operand plus a loop-invariant offset. Page numbers are clamped into
-  // the pool, so every staging load is in bounds, keys at or past hi included;
-  // V rows of those keys are replaced by zeros before they reach LDS (unwritten
-  // slots may hold NaN, and 0·NaN would poison the PV product), K rows of those
-  // keys only reach scores that the mask replaces by -inf.
-  static_assert(16 % (64 / CPR) == 0, "a wave's staging chunks must lie in one page");
+  // Staging: direct global -> LDS loads (global_load_lds_dwordx4). One load
+  // of a wave moves 64 chunks of 16 B into 1 KB of LDS, lane i to byte 16·i:
+  // block e = r·NW + w (r < PER_T) of a tile holds key rows RPB·e .. +RPB-1
+  // (RPB = 1024 / RB). Rows are unpadded; instead each row's 16-byte chunks are
+  // XOR-swizzled by the row's position in its page (rt = key mod 16):
+  //   K chunk c sits at c ^ (rt mod CPR)            (16 rows read per 16 lanes)
+  //   V chunk c sits at c ^ 2·(rt mod CPR/2)        (pairs stay adjacent for the
+  //                                                   32-byte transpose reads)
+  // so both read patterns are bank-conflict-free. Lane i loads the global
+  // chunk that belongs at its LDS position. Tiles start on page boundaries and
+  // NW·RPB is a multiple of 16, so rt and both source offsets are the same on
+  // every tile and every r; the page of block e is r·PG_STEP + (wave offset).
+  constexpr int RPB = 1024 / RB;
   constexpr int PAGES_PER_TILE = KT / 16;
-  // Chunk e lies in page e / (16·CPR) = e / (2D) of the tile: page
-  // r·PG_STEP + (wave's offset), known at compile time up to the wave.
   constexpr int PG_STEP = NW * 64 / (2 * D);
+  static_assert(RPB * PER_T * NW == KT, "a tile is PER_T loads per wave");
+  static_assert((NW * RPB) % 16 == 0, "row-in-page of a lane is the same for every r");
   static_assert(PG_STEP * 2 * D == NW * 64 && PG_STEP * PER_T == PAGES_PER_TILE, "staging page layout");
-  static_assert(PG_STEP == 1 || PG_STEP == 2, "a wave's chunks of one r lie in page r·PG_STEP + (0 or 1)");
+  static_assert(PG_STEP == 1 || PG_STEP == 2, "a wave's block of one r lies in page r·PG_STEP + (0 or 1)");
   const int pg_wave = uniform((int)(threadIdx.x / (2 * D)));  // always 0 when PG_STEP == 1
-  uint32_t st_off[PER_T];  // byte offset of the chunk inside its page
-  int st_key[PER_T];       // key of the chunk within the tile
-#pragma unroll
-  for (int r = 0; r < PER_T; ++r) {
-    const int e = threadIdx.x + r * NW * 64;
-    const int key = e / CPR;
-    const int part = e - key * CPR;
-    st_key[r] = key;
-    st_off[r] = (uint32_t)(((int64_t)(key & 15) * a.c_st + part * 8) * 2);
-  }
+  const int st_rt = (w * RPB + lane / CPR) & 15;             // the lane's row within its page
+  const int st_pos = lane % CPR;                              // the lane's chunk position in the row
+  const uint32_t st_off_k = (uint32_t)(((int64_t)st_rt * a.c_st + (st_pos ^ (st_rt & (CPR - 1))) * 8) * 2);
+  const uint32_t st_off_v =
+      (uint32_t)(((int64_t)st_rt * a.c_st + (st_pos ^ (2 * (st_rt & (CPR / 2 - 1)))) * 8) * 2);
+  const uint32_t lds_base = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) unsigned char*)lds);
+  const uint32_t lds_wave = lds_base + (uint32_t)w * 1024u;
 
   // The four page numbers of a tile, as scalar loads (constant address space)
   // issued together and consumed together: one wait for all four. Entries
@@ -239,9 +242,11 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   // reach there).
   typedef const int32_t __attribute__((address_space(4)))* ConstI32;
   const ConstI32 bts = (ConstI32)bt;
-  const uint32_t page_elems = (uint32_t)a.c_sb;  // < 2^31, checked on the host
-  auto page_bases = [&](int kt, int64_t (&po)[PAGES_PER_TILE]) {
-    int raw[PAGES_PER_TILE];
+  const uint32_t page_bytes = (uint32_t)a.c_sb * 2u;  // c_sb < 2^31, checked on the host
+  // page_fetch issues the scalar loads of tile kt's entries; page_finish
+  // waits for them (one wait for all four) and forms the byte offsets. A
+  // fetch issued a half step before its finish hides the load latency.
+  auto page_fetch = [&](int kt, int (&raw)[PAGES_PER_TILE]) __attribute__((always_inline)) {
     const int i0 = kt * PAGES_PER_TILE;
     if (i0 + PAGES_PER_TILE <= a.max_blocks) {
 #pragma unroll
@@ -250,53 +255,60 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
 #pragma unroll
       for (int pg = 0; pg < PAGES_PER_TILE; ++pg) raw[pg] = bts[min(i0 + pg, a.max_blocks - 1)];
     }
-    asm volatile("" ::"s"(raw[0]), "s"(raw[1]), "s"(raw[2]), "s"(raw[3]));
+  };
+  auto page_finish = [&](int (&raw)[PAGES_PER_TILE], int64_t (&po)[PAGES_PER_TILE]) __attribute__((always_inline)) {
+    asm volatile("" : "+s"(raw[0]), "+s"(raw[1]), "+s"(raw[2]), "+s"(raw[3]));
 #pragma unroll
     for (int pg = 0; pg < PAGES_PER_TILE; ++pg)
-      po[pg] = (int64_t)((uint64_t)(uint32_t)min(max(raw[pg], 0), a.num_pages - 1) * page_elems);
+      po[pg] = (int64_t)((uint64_t)(uint32_t)min(max(raw[pg], 0), a.num_pages - 1) * page_bytes);
+  };
+  auto page_bases = [&](int kt, int64_t (&po)[PAGES_PER_TILE]) __attribute__((always_inline)) {
+    int raw[PAGES_PER_TILE];
+    page_fetch(kt, raw);
+    page_finish(raw, po);
   };
   static_assert(PAGES_PER_TILE == 4, "page_bases consumes four entries");
 
-  // Staging loads are inline-asm global loads, waited for explicitly before
-  // their registers are stored to LDS: the compiler's own waitcnt insertion
-  // would drain them at the loop header, serialising the next tile's memory
-  // latency with the current tile's compute.
-  u32x4_t stk[PER_T], stv[PER_T];
-  auto stage_issue = [&](const int64_t (&po)[PAGES_PER_TILE]) {
+  // The loads are inline asm, invisible to the compiler's wait insertion
+  // (which would otherwise wait for them before every LDS read); each wave
+  // waits for its own loads (vmcnt) before the barrier that publishes a tile.
+  // M0 holds the wave's LDS destination.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  auto dma = [&](const unsigned char* gbase, uint32_t off, uint32_t lds_addr) __attribute__((always_inline)) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(lds_addr), "v"(off), "s"(gbase)
+                 : "memory", "m0");
+  };
+#pragma clang diagnostic pop
+  auto page_of = [&](const int64_t (&po)[PAGES_PER_TILE], int r) __attribute__((always_inline)) -> int64_t  {
+    if constexpr (PG_STEP == 1) return po[r];
+    else return pg_wave ? po[PG_STEP * r + 1] : po[PG_STEP * r];
+  };
+  auto stage_k = [&](const int64_t (&po)[PAGES_PER_TILE], int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int r = 0; r < PER_T; ++r) {
-      int64_t p;
-      if constexpr (PG_STEP == 1) p = po[r];
-      else p = pg_wave ? po[PG_STEP * r + 1] : po[PG_STEP * r];
-      const uint16_t* kb = kc + p;
-      const uint16_t* vb = vc + p;
-      asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(stk[r]) : "v"(st_off[r]), "s"(kb));
-      asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(stv[r]) : "v"(st_off[r]), "s"(vb));
+    for (int r = 0; r < PER_T; ++r) dma(kc + page_of(po, r), st_off_k, lds_wave + buf * TB + r * NW * 1024);
+  };
+  auto stage_v = [&](const int64_t (&po)[PAGES_PER_TILE], int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < PER_T; ++r) dma(vc + page_of(po, r), st_off_v, lds_wave + (2 + buf) * TB + r * NW * 1024);
+  };
+  // After the wave's loads landed: V rows of tile kt at or past hi become
+  // zeros (unwritten slots may hold NaN, and 0·NaN would poison the PV
+  // product). K rows there only reach scores that the mask replaces by -inf.
+  auto zero_v_tail = [&](int kt, int buf) __attribute__((always_inline)) {
+    if (kt * KT + KT > hi) {  // uniform
+#pragma unroll
+      for (int r = 0; r < PER_T; ++r) {
+        const int row = (r * NW + w) * RPB + lane / CPR;
+        if (kt * KT + row >= hi)
+          *reinterpret_cast<u32x4_t*>(lds + (2 + buf) * TB + (r * NW + w) * 1024 + lane * 16) =
+              u32x4_t{0u, 0u, 0u, 0u};
+      }
     }
   };
-  // Waits for the staging loads of tile kt, zeroes its V rows at or past hi and
-  // stores the tile into LDS buffer buf.
-  auto stage_finish = [&](int kt, int buf) {
-    if constexpr (PER_T == 4)
-      asm volatile("s_waitcnt vmcnt(0)"
-                   : "+v"(stk[0]), "+v"(stk[1]), "+v"(stk[2]), "+v"(stk[3]),
-                     "+v"(stv[0]), "+v"(stv[1]), "+v"(stv[2]), "+v"(stv[3]));
-    else
-      asm volatile("s_waitcnt vmcnt(0)" : "+v"(stk[0]), "+v"(stk[1]), "+v"(stv[0]), "+v"(stv[1]));
-    static_assert(PER_T == 4 || PER_T == 2, "staging wait covers 2 or 4 chunks");
-    if (kt * KT + KT > hi) {  // the tile reaches hi (uniform)
-#pragma unroll
-      for (int r = 0; r < PER_T; ++r)
-        if (kt * KT + st_key[r] >= hi) stv[r] = u32x4_t{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int r = 0; r < PER_T; ++r) {
-      const int e = threadIdx.x + r * NW * 64;
-      const int part = e - st_key[r] * CPR;
-      *reinterpret_cast<u32x4_t*>(&lds_k[buf][st_key[r] * PITCH + part * 8]) = stk[r];
-      *reinterpret_cast<u32x4_t*>(&lds_v[buf][st_key[r] * PITCH_V + part * 8]) = stv[r];
-    }
-  };
+  auto wait_loads = [&]() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
 
   // Last visible key of each column (its query position, at most hi - 1):
   // on tiles that reach past a column's diagonal or past hi, key pos is masked
@@ -304,125 +316,192 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   int lim[QT];
 #pragma unroll
   for (int ct = 0; ct < QT; ++ct) lim[ct] = min(qpos[ct], hi - 1);
+  // 32-key halves of tiles this wave computes: up to its last visible key
+  // (wave_hi) and below hi.
+  const int wave_halves = wave_live ? min((hi + 31) / 32, wave_hi / 32 + 1) : 0;
 
-  int64_t po[PAGES_PER_TILE];
-  if (n_tiles > 0) {
-    page_bases(0, po);
-    stage_issue(po);
-    stage_finish(0, 0);
-  }
-  __syncthreads();
-
-  // One key tile: stage tile kt + 1 into the idle buffer while tile kt computes.
-  // Staging runs on every tile, also the last: tile n_tiles is clamped into the
-  // pool like any other and its buffer is never read.
-  auto tile = [&](const int kt, const int buf) {
-    page_bases(kt + 1, po);
-    stage_issue(po);
-
-    if (wave_live && kt * KT <= wave_hi) {
-      const uint16_t* K = lds_k[buf];
-      const uint16_t* V = lds_v[buf];
-      f32x4_t sacc[QT][4];
+  // ---- products and softmax, per 32-key half of a 64-key tile ----
+  // Sᵀ of keys 32h .. 32h+31 of the tile in K buffer kbuf, for the wave's QT
+  // column tiles: S[ct][t'] holds keys 32h + 16t' + 4g + i (lane n = column).
+  auto qk = [&](f32x4_t (&S)[QT][2], int kbuf, const int h) __attribute__((always_inline)) {
+    const unsigned char* K = lds + kbuf * TB;
 #pragma unroll
-      for (int ct = 0; ct < QT; ++ct)
+    for (int ct = 0; ct < QT; ++ct)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) sacc[ct][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      // The MFMA runs are issued at raised wave priority: the SIMD's other wave
-      // (another work-group's, usually in its softmax) fills the VALU slots
-      // between them instead of delaying them.
-      __builtin_amdgcn_s_setprio(1);
+      for (int t = 0; t < 2; ++t) S[ct][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < 2; ++t) {
 #pragma unroll
-        for (int c = 0; c < KC; ++c) {
-          const uint4 ka = ld16(K + (16 * t + n) * PITCH + 8 * (4 * c + g));
+      for (int c = 0; c < KC; ++c) {
+        // row 32h + 16t + n (its row in page is n), chunk 4c + g
+        const uint4 ka = ld16(K + (32 * h + 16 * t + n) * RB + 16 * ((4 * c + g) ^ (n & (CPR - 1))));
 #pragma unroll
-          for (int ct = 0; ct < QT; ++ct) sacc[ct][t] = mfma_16x16x32(ka, qreg[ct][c], sacc[ct][t]);
-        }
+        for (int ct = 0; ct < QT; ++ct) S[ct][t] = mfma_16x16x32(ka, qreg[ct][c], S[ct][t]);
       }
-
-      __builtin_amdgcn_s_setprio(0);
-      uint4 pb[QT][2];
-      // Some key of the tile may be invisible to some column: past the causal
-      // diagonal of the wave's first query, or at/after hi.
-      const bool diag = (kt * KT + KT - 1 > ctx + wave_q0) || (kt * KT + KT > hi);
-#pragma unroll
-      for (int ct = 0; ct < QT; ++ct) {
-        // Raw scores; the scale (> 0, so the max commutes with it) is applied
-        // inside the exponent's fma: p = 2^(s·scale_log2 − m).
-        float sv[4][4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sv[t][i] = sacc[ct][t][i];
-        if (diag) {
-          // key 16t + 4g + i of the tile is masked iff 16t + i > lim - kt·KT - 4g.
-          const int rel = lim[ct] - kt * KT - 4 * g;
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (16 * t + i > rel) sv[t][i] = kNegInf;
-        }
-        float mx = kNegInf;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          mx = fmax_prop(mx, fmax_prop(fmax_prop(sv[t][0], sv[t][1]), fmax_prop(sv[t][2], sv[t][3])));
-        mx = max_across_groups(mx);
-        const float m_new = fmax_prop(m[ct], mx * a.scale_log2);
-        const float alpha = fast_exp2(m[ct] - m_new);
-        float p[4][4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) p[t][i] = fast_exp2(__builtin_fmaf(sv[t][i], a.scale_log2, -m_new));
-        float ps[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) ps[t] = (p[t][0] + p[t][1]) + (p[t][2] + p[t][3]);
-        const float psum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
-        l[ct] = l[ct] * alpha + psum;
-        m[ct] = m_new;
-        if (!wave_all_one(alpha)) {  // x·1 == x: skipping is exact
-#pragma unroll
-          for (int c = 0; c < VD; ++c) acc[ct][c] *= alpha;
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          pb[ct][u].x = pack_bf16x2_hw(p[2 * u][0], p[2 * u][1]);
-          pb[ct][u].y = pack_bf16x2_hw(p[2 * u][2], p[2 * u][3]);
-          pb[ct][u].z = pack_bf16x2_hw(p[2 * u + 1][0], p[2 * u + 1][1]);
-          pb[ct][u].w = pack_bf16x2_hw(p[2 * u + 1][2], p[2 * u + 1][3]);
-        }
-      }
-
-      // Vᵀ operand of dims 16c .. 16c+15 over keys 32u + {4g .. 4g+3, 16+4g .. 16+4g+3}
-      // (the keys whose P this lane holds): two transpose reads.
-      const int trow = 4 * g + (n >> 2);
-      const int tcol = 4 * (n & 3);
-      __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-#pragma unroll
-        for (int c = 0; c < VD; ++c) {
-          const uint2 lo = ld_tr16(V + (32 * u + trow) * PITCH_V + 16 * c + tcol);
-          const uint2 hi2 = ld_tr16(V + (32 * u + 16 + trow) * PITCH_V + 16 * c + tcol);
-          const uint4 va = make_uint4(lo.x, lo.y, hi2.x, hi2.y);
-#pragma unroll
-          for (int ct = 0; ct < QT; ++ct) acc[ct][c] = mfma_16x16x32(va, pb[ct][u], acc[ct][c]);
-        }
-      }
-      __builtin_amdgcn_s_setprio(0);
     }
-
-    stage_finish(kt + 1, buf ^ 1);
-    __syncthreads();
+  };
+  // Causal / hi mask of a half whose first key is k0 (absolute position):
+  // key k0 + 16t + 4g + i is masked iff 16t + i > lim - k0 - 4g.
+  auto mask = [&](f32x4_t (&S)[QT][2], int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ct = 0; ct < QT; ++ct) {
+      const int rel = lim[ct] - k0 - 4 * g;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (16 * t + i > rel) S[ct][t][i] = kNegInf;
+    }
+  };
+  // Some key of the half at k0 may be invisible to some column of the wave.
+  auto needs_mask = [&](int k0) { return (k0 + 31 > ctx + wave_q0) || (k0 + 32 > hi); };
+  // Running max of each column. The raw scores' max is scaled (scale > 0
+  // commutes with max) into log2 units. The max is updated lazily: while
+  // every lane's new max stays within 8 (a factor 256) of the running max, the
+  // running max is kept, alpha is exactly 1 and the rescale of acc is skipped;
+  // p = 2^(s·scale − m) then stays ≤ 256, far inside fp32 and bf16 range, and
+  // the final division by the row sum removes the common factor.
+  auto row_max = [&](const f32x4_t (&S)[QT][2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ct = 0; ct < QT; ++ct) {
+      float mx = fmax_prop(fmax_prop(fmax_prop(S[ct][0][0], S[ct][0][1]), fmax_prop(S[ct][0][2], S[ct][0][3])),
+                           fmax_prop(fmax_prop(S[ct][1][0], S[ct][1][1]), fmax_prop(S[ct][1][2], S[ct][1][3])));
+      mx = max_across_groups(mx);
+      const float m_t = mx * a.scale_log2;
+      const bool keep = __builtin_amdgcn_ballot_w64(!(m_t <= m[ct] + 8.0f)) == 0;
+      const float m_new = keep ? m[ct] : fmax_prop(m[ct], m_t);
+      alpha[ct] = fast_exp2(m[ct] - m_new);
+      m[ct] = m_new;
+    }
+  };
+  // P = 2^(s·scale − m), packed to bf16 as the B operand of the PV product
+  // over the half's 32 keys; the row sums accumulate into l.
+  auto softmax_p = [&](const f32x4_t (&S)[QT][2], uint4 (&pb)[QT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ct = 0; ct < QT; ++ct) {
+      float p[2][4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[t][i] = fast_exp2(__builtin_fmaf(S[ct][t][i], a.scale_log2, -m[ct]));
+      l[ct] = l[ct] * alpha[ct] + (((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) +
+                                   ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3])));
+      pb[ct].x = pack_bf16x2_hw(p[0][0], p[0][1]);
+      pb[ct].y = pack_bf16x2_hw(p[0][2], p[0][3]);
+      pb[ct].z = pack_bf16x2_hw(p[1][0], p[1][1]);
+      pb[ct].w = pack_bf16x2_hw(p[1][2], p[1][3]);
+    }
+  };
+  auto rescale = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int ct = 0; ct < QT; ++ct) {
+      if (!wave_all_one(alpha[ct])) {  // x·1 == x: skipping is exact
+#pragma unroll
+        for (int c = 0; c < VD; ++c) acc[ct][c] *= alpha[ct];
+      }
+    }
+  };
+  // Oᵀ += Vᵀ·Pᵀ over keys 32h .. 32h+31 of the tile in V buffer vbuf, V operand
+  // by transpose reads: dims 16c .. 16c+15 over keys 32h + {4g .. 4g+3,
+  // 16+4g .. 16+4g+3} (the keys whose P this lane holds). Lane n of group g
+  // addresses row 32h + 4g + n/4 (and +16), bytes 32c + 8(n mod 4) of the row,
+  // i.e. chunk 2c + (n mod 4)/2, stored at that chunk ^ 2·(row mod CPR/2).
+  const int tr_row = 4 * g + (n >> 2);
+  auto pv = [&](const uint4 (&pb)[QT], int vbuf, const int h) __attribute__((always_inline)) {
+    const unsigned char* V = lds + (2 + vbuf) * TB;
+    const int r0 = 32 * h + tr_row, r1 = r0 + 16;
+    const int sw0 = 2 * (r0 & (CPR / 2 - 1)), sw1 = 2 * (r1 & (CPR / 2 - 1));
+#pragma unroll
+    for (int c = 0; c < VD; ++c) {
+      const uint2 lo = ld_tr16(reinterpret_cast<const uint16_t*>(
+          V + r0 * RB + 16 * ((2 * c + ((n & 3) >> 1)) ^ sw0) + 8 * (n & 1)));
+      const uint2 hi2 = ld_tr16(reinterpret_cast<const uint16_t*>(
+          V + r1 * RB + 16 * ((2 * c + ((n & 3) >> 1)) ^ sw1) + 8 * (n & 1)));
+      const uint4 va = make_uint4(lo.x, lo.y, hi2.x, hi2.y);
+#pragma unroll
+      for (int ct = 0; ct < QT; ++ct) acc[ct][c] = mfma_16x16x32(va, pb[ct], acc[ct][c]);
+    }
   };
 
-  // Two tiles per iteration, so that each tile's LDS buffer is a constant.
-  for (int kt = 0; kt < n_tiles; kt += 2) {
-    tile(kt, 0);
-    if (kt + 1 < n_tiles) tile(kt + 1, 1);
+  // ---- pipeline over 32-key halves ----
+  // Half x = 2j + h is keys 32x .. 32x+31 (tile j, half h). Half step x
+  // computes Sᵀ(x+1) while forming P(x) from Sᵀ(x), rescales acc, masks
+  // Sᵀ(x+1) if needed, then accumulates PV(x) while taking the max of Sᵀ(x+1).
+  // Buffers: K(j) in K buffer j&1, V(j) in V buffer j&1. Per tile j:
+  //   start:  loads of V(j+1) into V buffer (j+1)&1 (V(j-1) is consumed);
+  //   half 0: reads K(j) (its second half) and V(j);
+  //   mid:    waits for K(j+1) (loaded since the previous mid), barrier —
+  //           K(j+1) is published and K(j) is consumed everywhere — then
+  //           loads K(j+2) into K buffer j&1;
+  //   half 1: reads K(j+1) (its first half) and V(j);
+  //   end:    waits for V(j+1), clears its rows past hi, barrier.
+  // Loads are waited for in issue order (vmcnt), one tile step after issue.
+  int64_t po_v[PAGES_PER_TILE], po_k[PAGES_PER_TILE];
+  f32x4_t S0[QT][2], S1[QT][2];
+  if (n_tiles > 0) {
+    page_bases(0, po_v);
+    stage_k(po_v, 0);
+    stage_v(po_v, 0);
+    page_bases(1, po_k);
+    stage_k(po_k, 1);
+    wait_loads();
+    zero_v_tail(0, 0);
+#pragma unroll
+    for (int pg = 0; pg < PAGES_PER_TILE; ++pg) po_v[pg] = po_k[pg];
+  }
+  __syncthreads();
+  if (wave_halves > 0) {
+    qk(S0, 0, 0);
+    if (needs_mask(0)) mask(S0, 0);
+    row_max(S0);
+  }
+
+  // Half step x (= 2j + h) on S(x) in Sc, producing S(x+1) in Sn.
+  auto half_step = [&](const int x, f32x4_t (&Sc)[QT][2], f32x4_t (&Sn)[QT][2], const int kbuf_next,
+                       const int h_next, const int vbuf, const int h) __attribute__((always_inline)) {
+    // One code path for every computed half: the last half also forms
+    // Sᵀ(x+1) (in-bounds LDS reads of a buffer it never uses), so that the
+    // accumulators have a single definition per step.
+    uint4 pb[QT];
+    if (x < wave_halves) {
+      __builtin_amdgcn_s_setprio(1);
+      qk(Sn, kbuf_next, h_next);
+      softmax_p(Sc, pb);
+      // P is formed here, under the QKᵀ MFMAs, not sunk past the branches below.
+#pragma unroll
+      for (int ct = 0; ct < QT; ++ct) asm volatile("" ::"v"(pb[ct].x), "v"(pb[ct].y), "v"(pb[ct].z), "v"(pb[ct].w));
+      __builtin_amdgcn_s_setprio(0);
+      rescale();
+      if (needs_mask(32 * (x + 1))) mask(Sn, 32 * (x + 1));
+      __builtin_amdgcn_s_setprio(1);
+      pv(pb, vbuf, h);
+      row_max(Sn);
+      __builtin_amdgcn_s_setprio(0);
+    }
+  };
+  auto wait_older_loads = [&]() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_T) : "memory"); };
+  // po_v holds the pages of tile j+1 (staged for K(j+1) at the previous mid
+  // step) when step j starts.
+  auto tile_step = [&](const int j, const int b) __attribute__((always_inline)) {  // b = j & 1
+    int raw[PAGES_PER_TILE];
+    page_fetch(j + 2, raw);
+    stage_v(po_v, b ^ 1);
+    half_step(2 * j, S0, S1, b, 1, b, 0);
+    wait_older_loads();  // K(j+1)
+    __syncthreads();
+    page_finish(raw, po_k);
+    stage_k(po_k, b);
+    half_step(2 * j + 1, S1, S0, b ^ 1, 0, b, 1);
+    wait_older_loads();  // V(j+1)
+    zero_v_tail(j + 1, b ^ 1);
+    __syncthreads();
+#pragma unroll
+    for (int pg = 0; pg < PAGES_PER_TILE; ++pg) po_v[pg] = po_k[pg];
+  };
+  // Two tiles per iteration, so that buffer numbers are constants.
+  for (int j = 0; j < n_tiles; j += 2) {
+    tile_step(j, 0);
+    if (j + 1 < n_tiles) tile_step(j + 1, 1);
   }
 
 #pragma unroll
