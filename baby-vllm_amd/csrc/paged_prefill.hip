@@ -16,9 +16,12 @@
 //   Sᵀ[16 keys × 16 cols] = K · Qᵀ       (K operand from LDS)
 //   Oᵀ[D × 16 cols]      += Vᵀ · Pᵀ      (Pᵀ from the Sᵀ registers, Vᵀ by LDS
 //                                         transpose reads)
-// software-pipelined by half: Sᵀ of the next half is computed while P of the
-// current half is formed, and the current PV product runs while the next
-// half's row max is taken, so MFMA and VALU work of one wave overlap.
+// software-pipelined by half: Sᵀ of the next half is computed while P and the
+// max of the current half are formed, so MFMA and VALU work of one wave
+// overlap. P uses the running max as its reference; only when a half's max
+// exceeds it by more than 8 (log2 units) is the max raised and P formed
+// again, so the max never delays P. The row sums come from an MFMA of P with
+// an all-ones operand, next to the PV product.
 // Keys at or past hi = min(seq_len, ctx + last query + 1) are masked, and their
 // V rows are zeroed in LDS, so cache slots that were never written (possibly
 // NaN) never reach a product.
@@ -193,16 +196,19 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
 #pragma unroll
     for (int c = 0; c < KC; ++c) asm volatile("" ::"v"(qreg[ct][c].x), "v"(qreg[ct][c].y), "v"(qreg[ct][c].z), "v"(qreg[ct][c].w));
 
-  float m[QT], l[QT], alpha[QT];
-  f32x4_t acc[QT][VD];
+  // lsum[ct]: the running row sums of P, accumulated by an MFMA of an all-ones
+  // operand with the same bf16 P that multiplies V (every row of the result
+  // holds the column sums), so numerator and denominator sum the same values.
+  float m[QT];
+  f32x4_t acc[QT][VD], lsum[QT];
 #pragma unroll
   for (int ct = 0; ct < QT; ++ct) {
     m[ct] = kNegInf;
-    l[ct] = 0.f;
-    alpha[ct] = 1.f;
+    lsum[ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < VD; ++c) acc[ct][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
+  const uint4 ones_bf16 = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
 
   const unsigned char* kc = reinterpret_cast<const unsigned char*>(a.k_cache) + (int64_t)kvh * a.c_sh * 2;
   const unsigned char* vc = reinterpret_cast<const unsigned char*>(a.v_cache) + (int64_t)kvh * a.c_sh * 2;
@@ -323,8 +329,11 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   // ---- products and softmax, per 32-key half of a 64-key tile ----
   // Sᵀ of keys 32h .. 32h+31 of the tile in K buffer kbuf, for the wave's QT
   // column tiles: S[ct][t'] holds keys 32h + 16t' + 4g + i (lane n = column).
+  uint32_t k_off[KC];  // row n (its row in page is n), chunk 4c + g
+#pragma unroll
+  for (int c = 0; c < KC; ++c) k_off[c] = (uint32_t)(n * RB + 16 * ((4 * c + g) ^ (n & (CPR - 1))));
   auto qk = [&](f32x4_t (&S)[QT][2], int kbuf, const int h) __attribute__((always_inline)) {
-    const unsigned char* K = lds + kbuf * TB;
+    const unsigned char* K = lds + kbuf * TB + 32 * h * RB;
 #pragma unroll
     for (int ct = 0; ct < QT; ++ct)
 #pragma unroll
@@ -333,8 +342,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
       for (int c = 0; c < KC; ++c) {
-        // row 32h + 16t + n (its row in page is n), chunk 4c + g
-        const uint4 ka = ld16(K + (32 * h + 16 * t + n) * RB + 16 * ((4 * c + g) ^ (n & (CPR - 1))));
+        const uint4 ka = ld16(K + 16 * t * RB + k_off[c]);
 #pragma unroll
         for (int ct = 0; ct < QT; ++ct) S[ct][t] = mfma_16x16x32(ka, qreg[ct][c], S[ct][t]);
       }
@@ -355,72 +363,81 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   };
   // Some key of the half at k0 may be invisible to some column of the wave.
   auto needs_mask = [&](int k0) { return (k0 + 31 > ctx + wave_q0) || (k0 + 32 > hi); };
-  // Running max of each column. The raw scores' max is scaled (scale > 0
-  // commutes with max) into log2 units. The max is updated lazily: while
-  // every lane's new max stays within 8 (a factor 256) of the running max, the
-  // running max is kept, alpha is exactly 1 and the rescale of acc is skipped;
-  // p = 2^(s·scale − m) then stays ≤ 256, far inside fp32 and bf16 range, and
-  // the final division by the row sum removes the common factor.
-  auto row_max = [&](const f32x4_t (&S)[QT][2]) __attribute__((always_inline)) {
+  // The scores' max of each column over a half, in log2 units (the scale is
+  // > 0, so it commutes with the max): a chain of three-input maxima, then
+  // across the four lane groups.
+  auto half_max = [&](const f32x4_t (&S)[QT][2], float (&mt)[QT]) __attribute__((always_inline)) {
 #pragma unroll
     for (int ct = 0; ct < QT; ++ct) {
-      float mx = fmax_prop(fmax_prop(fmax_prop(S[ct][0][0], S[ct][0][1]), fmax_prop(S[ct][0][2], S[ct][0][3])),
-                           fmax_prop(fmax_prop(S[ct][1][0], S[ct][1][1]), fmax_prop(S[ct][1][2], S[ct][1][3])));
-      mx = max_across_groups(mx);
-      const float m_t = mx * a.scale_log2;
-      const bool keep = __builtin_amdgcn_ballot_w64(!(m_t <= m[ct] + 8.0f)) == 0;
-      const float m_new = keep ? m[ct] : fmax_prop(m[ct], m_t);
-      alpha[ct] = fast_exp2(m[ct] - m_new);
-      m[ct] = m_new;
+      float mx = fmax_prop(fmax_prop(S[ct][0][0], S[ct][0][1]), S[ct][0][2]);
+      mx = fmax_prop(fmax_prop(mx, S[ct][0][3]), S[ct][1][0]);
+      mx = fmax_prop(fmax_prop(mx, S[ct][1][1]), S[ct][1][2]);
+      mx = fmax_prop(mx, S[ct][1][3]);
+      mt[ct] = max_across_groups(mx) * a.scale_log2;
     }
   };
   // P = 2^(s·scale − m), packed to bf16 as the B operand of the PV product
-  // over the half's 32 keys; the row sums accumulate into l.
+  // over the half's 32 keys.
+  auto softmax_p1 = [&](const f32x4_t (&S)[QT][2], uint4 (&pb)[QT], const int ct) __attribute__((always_inline)) {
+    float p[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[t][i] = fast_exp2(__builtin_fmaf(S[ct][t][i], a.scale_log2, -m[ct]));
+    pb[ct].x = pack_bf16x2_hw(p[0][0], p[0][1]);
+    pb[ct].y = pack_bf16x2_hw(p[0][2], p[0][3]);
+    pb[ct].z = pack_bf16x2_hw(p[1][0], p[1][1]);
+    pb[ct].w = pack_bf16x2_hw(p[1][2], p[1][3]);
+  };
   auto softmax_p = [&](const f32x4_t (&S)[QT][2], uint4 (&pb)[QT]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int ct = 0; ct < QT; ++ct) {
-      float p[2][4];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) p[t][i] = fast_exp2(__builtin_fmaf(S[ct][t][i], a.scale_log2, -m[ct]));
-      l[ct] = l[ct] * alpha[ct] + (((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) +
-                                   ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3])));
-      pb[ct].x = pack_bf16x2_hw(p[0][0], p[0][1]);
-      pb[ct].y = pack_bf16x2_hw(p[0][2], p[0][3]);
-      pb[ct].z = pack_bf16x2_hw(p[1][0], p[1][1]);
-      pb[ct].w = pack_bf16x2_hw(p[1][2], p[1][3]);
-    }
+    for (int ct = 0; ct < QT; ++ct) softmax_p1(S, pb, ct);
   };
-  auto rescale = [&]() __attribute__((always_inline)) {
+  // The running max m is the reference of P = 2^(s·scale − m). It is raised
+  // only when some column's new max exceeds it by more than 8 (a factor 256;
+  // P stays far inside fp32 and bf16 range, and the final division by the
+  // row sum removes the common factor): then acc and the row sums are
+  // rescaled by 2^(m_old − m_new) and P is formed again. So P does not wait
+  // for the max, which is computed alongside it and only gates this rare path.
+  auto raise_max = [&](const f32x4_t (&S)[QT][2], const float (&mt)[QT], uint4 (&pb)[QT]) __attribute__((always_inline)) {
 #pragma unroll
     for (int ct = 0; ct < QT; ++ct) {
-      if (!wave_all_one(alpha[ct])) {  // x·1 == x: skipping is exact
+      if (__builtin_amdgcn_ballot_w64(!(mt[ct] <= m[ct] + 8.0f)) != 0) {
+        const float m_new = fmax_prop(m[ct], mt[ct]);
+        const float alpha = fast_exp2(m[ct] - m_new);
+        m[ct] = m_new;
 #pragma unroll
-        for (int c = 0; c < VD; ++c) acc[ct][c] *= alpha[ct];
+        for (int c = 0; c < VD; ++c) acc[ct][c] *= alpha;
+        lsum[ct] *= alpha;
+        softmax_p1(S, pb, ct);
       }
     }
   };
-  // Oᵀ += Vᵀ·Pᵀ over keys 32h .. 32h+31 of the tile in V buffer vbuf, V operand
-  // by transpose reads: dims 16c .. 16c+15 over keys 32h + {4g .. 4g+3,
-  // 16+4g .. 16+4g+3} (the keys whose P this lane holds). Lane n of group g
-  // addresses row 32h + 4g + n/4 (and +16), bytes 32c + 8(n mod 4) of the row,
-  // i.e. chunk 2c + (n mod 4)/2, stored at that chunk ^ 2·(row mod CPR/2).
-  const int tr_row = 4 * g + (n >> 2);
+  // Lane n of group g addresses row 32h + 4g + n/4 (and +16), bytes
+  // 32c + 8(n mod 4), i.e. chunk 2c + (n mod 4)/2, stored at that chunk ^
+  // 2·(row mod CPR/2); 32h and 16 do not change the row's swizzle, so the
+  // lane's offset for dim block c is fixed and h, +16 and the buffer enter as
+  // constants.
+  uint32_t v_off[VD];
+  {
+    const int tr_row = 4 * g + (n >> 2);
+    const int sw = 2 * (tr_row & (CPR / 2 - 1));
+#pragma unroll
+    for (int c = 0; c < VD; ++c)
+      v_off[c] = (uint32_t)(tr_row * RB + 16 * ((2 * c + ((n & 3) >> 1)) ^ sw) + 8 * (n & 1));
+  }
   auto pv = [&](const uint4 (&pb)[QT], int vbuf, const int h) __attribute__((always_inline)) {
-    const unsigned char* V = lds + (2 + vbuf) * TB;
-    const int r0 = 32 * h + tr_row, r1 = r0 + 16;
-    const int sw0 = 2 * (r0 & (CPR / 2 - 1)), sw1 = 2 * (r1 & (CPR / 2 - 1));
+    const unsigned char* V = lds + (2 + vbuf) * TB + 32 * h * RB;
 #pragma unroll
     for (int c = 0; c < VD; ++c) {
-      const uint2 lo = ld_tr16(reinterpret_cast<const uint16_t*>(
-          V + r0 * RB + 16 * ((2 * c + ((n & 3) >> 1)) ^ sw0) + 8 * (n & 1)));
-      const uint2 hi2 = ld_tr16(reinterpret_cast<const uint16_t*>(
-          V + r1 * RB + 16 * ((2 * c + ((n & 3) >> 1)) ^ sw1) + 8 * (n & 1)));
+      const uint2 lo = ld_tr16(reinterpret_cast<const uint16_t*>(V + v_off[c]));
+      const uint2 hi2 = ld_tr16(reinterpret_cast<const uint16_t*>(V + 16 * RB + v_off[c]));
       const uint4 va = make_uint4(lo.x, lo.y, hi2.x, hi2.y);
 #pragma unroll
       for (int ct = 0; ct < QT; ++ct) acc[ct][c] = mfma_16x16x32(va, pb[ct], acc[ct][c]);
     }
+#pragma unroll
+    for (int ct = 0; ct < QT; ++ct) lsum[ct] = mfma_16x16x32(ones_bf16, pb[ct], lsum[ct]);
   };
 
   // ---- pipeline over 32-key halves ----
@@ -453,7 +470,12 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   if (wave_halves > 0) {
     qk(S0, 0, 0);
     if (needs_mask(0)) mask(S0, 0);
-    row_max(S0);
+    // The first half's max is the first reference; a column with no visible
+    // key yet takes 0 (its P is then 0, and a later max above 8 raises it).
+    float mt[QT];
+    half_max(S0, mt);
+#pragma unroll
+    for (int ct = 0; ct < QT; ++ct) m[ct] = mt[ct] == kNegInf ? 0.f : mt[ct];
   }
 
   // Half step x (= 2j + h) on S(x) in Sc, producing S(x+1) in Sn.
@@ -464,18 +486,20 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
     // accumulators have a single definition per step.
     uint4 pb[QT];
     if (x < wave_halves) {
+      float mt[QT];
       __builtin_amdgcn_s_setprio(1);
       qk(Sn, kbuf_next, h_next);
       softmax_p(Sc, pb);
-      // P is formed here, under the QKᵀ MFMAs, not sunk past the branches below.
+      half_max(Sc, mt);
+      // P is formed here, under the QKᵀ MFMAs and beside the max, not sunk
+      // past the branches below.
 #pragma unroll
       for (int ct = 0; ct < QT; ++ct) asm volatile("" ::"v"(pb[ct].x), "v"(pb[ct].y), "v"(pb[ct].z), "v"(pb[ct].w));
       __builtin_amdgcn_s_setprio(0);
-      rescale();
+      raise_max(Sc, mt, pb);
       if (needs_mask(32 * (x + 1))) mask(Sn, 32 * (x + 1));
       __builtin_amdgcn_s_setprio(1);
       pv(pb, vbuf, h);
-      row_max(Sn);
       __builtin_amdgcn_s_setprio(0);
     }
   };
@@ -503,10 +527,13 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
     tile_step(j, 0);
     if (j + 1 < n_tiles) tile_step(j + 1, 1);
   }
+  // The last step's prefetch into LDS is still in flight: it must land
+  // before the work-group ends and its LDS is handed to another.
+  wait_loads();
 
 #pragma unroll
   for (int ct = 0; ct < QT; ++ct) {
-    const float lt = sum_across_groups(l[ct]);
+    const float lt = lsum[ct][0];
     if (!valid[ct]) continue;
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     // acc[ct][c][i] is dim 16c + 4g + i.
