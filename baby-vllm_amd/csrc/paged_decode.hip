@@ -20,6 +20,17 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
   decode_work_group<D, NW, PF>(a, blockIdx.x, smem);
 }
 
+// Many short splits: one split per wave (decode_split_wave), four independent
+// waves per work-group.
+template <int D, int PF>
+__global__ __launch_bounds__(256, 2) void paged_decode_split_wave_kernel(DecodeArgs a, int items) {
+  __shared__ __attribute__((aligned(16))) unsigned char tiles[4 * kTileBytes<D>];
+  const int w = wave_id();
+  const int item = (int)blockIdx.x * 4 + w;
+  if (item >= items) return;
+  decode_split_wave<D, PF>(a, item, tiles + w * kTileBytes<D>);
+}
+
 // Split reduce: out = Σ_s w_s·o_s / Σ_s w_s, w_s = 2^(lse_s − max lse), over the
 // S partial states of a (row, head). Both reduce kernels use the same
 // arithmetic, so a row's bits do not depend on S beyond its empty splits
@@ -220,9 +231,35 @@ static int decode_splits_per_wg(const DecodeArgs& a, int nw) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(gps, a.num_splits));
 }
 
+// Splits of at most this many pages run one per wave (decode_split_wave):
+// with 4 or 8 pages per split the work-group path spends most of a split in
+// its cross-wave merge. BVLLM_DECODE_SPLIT_WAVES=0 / 1 forces the work-group
+// / the per-wave path for any split plan (read per launch: tests vary it).
+constexpr int kSplitWaveMaxPages = 8;
+static bool use_split_waves(const DecodeArgs& a) {
+  if (a.num_splits <= 1 || a.waves != 4 || a.query_start_loc != nullptr) return false;
+  const char* env = getenv("BVLLM_DECODE_SPLIT_WAVES");
+  if (env && env[0] == '0') return false;
+  if (env && env[0] == '1') return true;
+  return a.blocks_per_split <= kSplitWaveMaxPages;
+}
+
+template <int D>
+static hipError_t launch_split_waves(const DecodeArgs& a, hipStream_t stream) {
+  const int64_t items = (int64_t)a.batch * a.num_kv_heads * a.num_splits;
+  if (items == 0) return hipSuccess;
+  if (items > 0x7ffffff0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((paged_decode_split_wave_kernel<D, 2>), dim3((unsigned)((items + 3) / 4)), dim3(256), 0,
+                     stream, a, (int)items);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  return launch_reduce<D>(a, stream);
+}
+
 template <int D, int NW, int PF>
 static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
   DecodeArgs a = args;
+  if (use_split_waves(a)) return launch_split_waves<D>(a, stream);
   a.splits_per_wg = decode_splits_per_wg(a, NW);
   const int G = a.num_heads / a.num_kv_heads;
   const size_t smem = decode_lds_bytes<D, NW>(G);

@@ -375,4 +375,134 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
   for (; j_cur < j1; ++j_cur) finish_split(j_cur);
 }
 
+// One split of one (sequence, KV head) on a single wave, for plans with many
+// short splits. The wave keeps the NW = 4 states that the waves of a
+// decode_work_group would keep (state s takes the split's pages start + s,
+// start + s + 4, ...), computes each page with the same process_page, and
+// merges the four states in registers with merge_states' arithmetic (max in
+// state order, then fma chains in state order), so the bits equal those of
+// decode_work_group for the same split. No LDS merge records and no
+// barriers: the waves of a work-group are independent. `tile` is the wave's
+// private K transpose tile (kTileBytes<D> bytes).
+template <int D, int PF>
+__device__ __forceinline__ void decode_split_wave(const DecodeArgs& a, const int item, unsigned char* tile) {
+  constexpr int KC = D / 32;
+  constexpr int VD = D / 16;
+  constexpr int NS = 4;  // the states of a 4-wave work-group
+  static_assert(PF == 2 || PF == 4, "pages in flight per wave");
+
+  const int G = a.num_heads / a.num_kv_heads;
+  const int split = item % a.num_splits;
+  const int bk = item / a.num_splits;
+  const int kvh = bk % a.num_kv_heads;
+  const int b = bk / a.num_kv_heads;
+
+  const int lane = lane_id();
+  const int n = lane & 15;
+  const int g = lane >> 4;
+
+  const int seq_len = uniform(a.seq_lens[b]);
+  int n_blocks = seq_len > 0 ? (seq_len + 15) / 16 : 0;
+  n_blocks = min(n_blocks, a.max_blocks);
+  const int start = split * a.blocks_per_split;
+  // The last split of the row runs to the row's last page.
+  const int end = (split == a.num_splits - 1) ? n_blocks : min(start + a.blocks_per_split, n_blocks);
+  const int cnt = max(end - start, 0);
+
+  uint4 qb[KC];
+  {
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_sb +
+                           (int64_t)(kvh * G + n) * a.q_sh;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) qb[c] = (n < G) ? ld16(qrow + 8 * (4 * c + g)) : make_uint4(0, 0, 0, 0);
+  }
+
+  WaveState<D> st[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    st[s].m = kNegInf;
+    st[s].l = 0.f;
+#pragma unroll
+    for (int c = 0; c < VD; ++c) st[s].acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  uint32_t off[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) off[j] = (uint32_t)((4 * g + j) * a.c_st + VD * n);
+  const uint16_t* kc = reinterpret_cast<const uint16_t*>(a.k_cache) + (int64_t)kvh * a.c_sh;
+  const uint16_t* vc = reinterpret_cast<const uint16_t*>(a.v_cache) + (int64_t)kvh * a.c_sh;
+  const int32_t* bt = a.block_tables + (int64_t)b * a.bt_stride;
+
+  // Pages are taken four at a time (one per state), PF in flight; loads are
+  // issued for clamped page indices, and pages past the split's end are
+  // skipped (a fully masked page would leave its state bit-identical anyway).
+  for (int base = 0; base < cnt; base += 64) {
+    const int here = min(64, cnt - base);
+    const int ent = bt[min(start + base + lane, a.max_blocks - 1)];
+    const int slot_ent = min(max(ent, 0), a.num_pages - 1);
+    auto phys = [&](int k) -> int64_t { return (int64_t)__builtin_amdgcn_readlane(slot_ent, k); };
+    PageRegs<D> r[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int64_t p = phys(min(i, here - 1)) * a.c_sb;
+      load_page<D>(r[i], kc + p, vc + p, off);
+    }
+    const int padded = (here + NS - 1) / NS * NS;
+    for (int k = 0; k < padded; k += NS) {
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        wait_page<(PF - 1) * kLoadsPerPage, D>(r[i % PF]);
+        const int page = start + base + k + i;
+        if (k + i < here)
+          process_page<D>(st[i], r[i % PF], qb, tile, n, g, page * 16 + 4 * g, seq_len, a.scale_log2);
+        const int64_t pn = phys(min(k + i + PF, here - 1)) * a.c_sb;
+        load_page<D>(r[i % PF], kc + pn, vc + pn, off);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PF; ++i) wait_page<0, D>(r[i]);
+  }
+
+  // merge_states' arithmetic, per lane: head n, dims (D/16)·(4g+i) + c.
+  float lt[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) lt[s] = sum_across_groups(st[s].l);
+  float M = kNegInf;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) M = fmaxf(M, st[s].m);
+  float L = 0.f;
+  f32x4_t A[VD];
+#pragma unroll
+  for (int c = 0; c < VD; ++c) A[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if (M != kNegInf) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const float wgt = fast_exp2(st[s].m - M);
+      L = __builtin_fmaf(lt[s], wgt, L);
+#pragma unroll
+      for (int c = 0; c < VD; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) A[c][i] = __builtin_fmaf(st[s].acc[c][i], wgt, A[c][i]);
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  if (n >= G) return;
+  const int head = kvh * G + n;
+  const int64_t prow = ((int64_t)b * a.num_heads + head) * a.num_splits + split;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float o[VD];
+#pragma unroll
+    for (int c = 0; c < VD; ++c) o[c] = L == 0.f ? 0.f : A[c][i] * inv;
+    float* dst = a.part_out + prow * D + VD * (4 * g + i);
+    if constexpr (VD == 8) {
+      *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
+    } else {
+      *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+  }
+  if (g == 0) a.part_lse[prow] = (L > 0.f) ? M + __log2f(L) : kNegInf;
+}
+
 }  // namespace bvllm

@@ -215,6 +215,7 @@ def test_splits_per_work_group_do_not_change_bits(lens, monkeypatch):
     from babyvllm.kernels.decode_split import DECODE_PARTITION_ENV
 
     monkeypatch.delenv(DECODE_PARTITION_ENV, raising=False)
+    monkeypatch.setenv("BVLLM_DECODE_SPLIT_WAVES", "0")  # the work-group path
     scale = HEAD_DIM ** -0.5
     q, kv_cache, bt, seq_lens = make_decode_inputs(lens, width=300, seed=len(lens))
     outs = []
@@ -225,3 +226,35 @@ def test_splits_per_work_group_do_not_change_bits(lens, monkeypatch):
         assert torch.equal(out, outs[0])
     assert not torch.isnan(outs[0]).any()
     assert_attn_close(outs[0], _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
+
+
+@pytest.mark.parametrize("partition", [1, 2, 3, 4, 7, 8, 16])
+@pytest.mark.parametrize("lens", [[600, 37, 0, 1], [2047, 16, 64, 300], [5000, 129]])
+def test_split_per_wave_matches_work_group_bits(partition, lens, monkeypatch):
+    """Short splits run one per wave, which keeps the four per-wave states of a
+    work-group in registers and merges them with the work-group's arithmetic:
+    the bits equal those of the work-group path for every split plan, also for
+    a row longer than the bucket (its last split runs to the row's end)."""
+    from babyvllm.kernels.decode_split import DECODE_PARTITION_ENV
+
+    monkeypatch.delenv(DECODE_PARTITION_ENV, raising=False)
+    scale = HEAD_DIM ** -0.5
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, width=320, seed=partition + len(lens))
+    outs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("BVLLM_DECODE_SPLIT_WAVES", mode)
+        outs[mode] = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=4096, partition_blocks=partition)
+    assert torch.equal(outs["0"], outs["1"])
+    assert not torch.isnan(outs["1"]).any()
+    assert_attn_close(outs["1"], _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
+
+
+@pytest.mark.parametrize("hkv,group,d", [(2, 7, 64), (1, 16, 128), (8, 4, 128)])
+def test_split_per_wave_other_head_configs(hkv, group, d, monkeypatch):
+    monkeypatch.setenv("BVLLM_DECODE_SPLIT_WAVES", "1")
+    lens = [700, 33, 0, 1500]
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, width=128, seed=hkv * 10 + group, hkv=hkv, group=group,
+                                                   d=d)
+    scale = d ** -0.5
+    out = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=2048, partition_blocks=4)
+    assert_attn_close(out, _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
