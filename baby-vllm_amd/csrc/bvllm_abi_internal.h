@@ -100,5 +100,7 @@ hipError_t paged_decode(const DecodeArgs& a, hipStream_t stream);
 // Partial states (per row and head) one decode launch writes to the workspace.
 int32_t decode_partials(const DecodeArgs& a);
 hipError_t paged_prefill(const PrefillArgs& a, hipStream_t stream);
+// Compute units of the current device (cached per device).
+int device_cus();
 
 }  // namespace bvllm

@@ -199,7 +199,7 @@ static hipError_t launch_reduce(const DecodeArgs& r, hipStream_t stream) {
 }
 
 // Compute units of the current device (cached per device).
-static int device_cus() {
+int device_cus() {
   static int cached[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;

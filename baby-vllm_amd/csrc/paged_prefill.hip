@@ -188,13 +188,6 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
       qreg[ct][c] = valid[ct] ? ld16(qrow + 8 * (4 * c + g)) : make_uint4(0, 0, 0, 0);
   }
 
-  // Make the Q loads complete here, once: otherwise they look pending at the
-  // key loop's header and the compiler drains every load there, including the
-  // next tile's staging loads, on each iteration.
-#pragma unroll
-  for (int ct = 0; ct < QT; ++ct)
-#pragma unroll
-    for (int c = 0; c < KC; ++c) asm volatile("" ::"v"(qreg[ct][c].x), "v"(qreg[ct][c].y), "v"(qreg[ct][c].z), "v"(qreg[ct][c].w));
 
   // lsum[ct]: the running row sums of P, accumulated by an MFMA of an all-ones
   // operand with the same bf16 P that multiplies V (every row of the result
@@ -466,6 +459,13 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
 #pragma unroll
     for (int pg = 0; pg < PAGES_PER_TILE; ++pg) po_v[pg] = po_k[pg];
   }
+  // The Q loads complete here, once, after the first tiles' table fetch and
+  // loads were issued behind them: otherwise they look pending at the key
+  // loop's header and the compiler drains every load there on each iteration.
+#pragma unroll
+  for (int ct = 0; ct < QT; ++ct)
+#pragma unroll
+    for (int c = 0; c < KC; ++c) asm volatile("" ::"v"(qreg[ct][c].x), "v"(qreg[ct][c].y), "v"(qreg[ct][c].z), "v"(qreg[ct][c].w));
   __syncthreads();
   if (wave_halves > 0) {
     qk(S0, 0, 0);
@@ -570,10 +570,17 @@ static DecodeArgs single_query_view(const PrefillArgs& p) {
   return a;
 }
 
-template <int D, int NW, int QT>
-static hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
-  const int G = a.num_heads / a.num_kv_heads;
-  const int64_t QB = NW * QT * (16 / G);
+// Launch geometry of a prefill batch for QB query rows per work-group.
+struct PrefillGrid {
+  int64_t bound = 0;  // query-block numbers
+  int dense_qb = 0;   // > 0: dense numbering with this many blocks per sequence
+  int xcd_group = 0;
+  int64_t per_xcd = 0;
+  int64_t prefill_wgs = 0, dec_wgs = 0;
+};
+
+static PrefillGrid plan_prefill(const PrefillArgs& a, int64_t QB) {
+  PrefillGrid p;
   // Upper bound of the query-block count: Σ ceil(q_s / QB) ≤ (T + S·(QB-1)) / QB
   // over the sequences the prefill work-groups compute.
   int64_t T = a.num_tokens, S = a.num_seqs;
@@ -581,35 +588,51 @@ static hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
     T -= a.single_query_seqs;
     S -= a.single_query_seqs;
   }
-  int64_t bound = S > 0 ? (T + S * (QB - 1)) / QB : 0;
+  p.bound = S > 0 ? (T + S * (QB - 1)) / QB : 0;
   // Query blocks are numbered densely (ceil(max_query_len / QB) per sequence,
   // found by division) unless that wastes more than a quarter of the grid on
   // empty blocks, as in a mixed step; then compactly (found by a scan).
   const int64_t dense = (a.max_query_len + QB - 1) / QB;
-  int dense_qb = 0;
-  if (dense * a.num_seqs * 4 <= bound * 5) {
-    dense_qb = (int)dense;
-    bound = dense * a.num_seqs;
+  if (dense * a.num_seqs * 4 <= p.bound * 5) {
+    p.dense_qb = (int)dense;
+    p.bound = dense * a.num_seqs;
   }
-  int xcd_group = (a.num_kv_heads <= 8 && 8 % a.num_kv_heads == 0) ? 8 / a.num_kv_heads : 0;
-  if (dense_qb > 0 && (int64_t)a.num_seqs * a.num_kv_heads >= 64) xcd_group = -1;
-  const int64_t per_xcd = (bound * a.num_kv_heads + 7) / 8;
-  const int64_t prefill_wgs = xcd_group > 0 ? 8 * ((bound + xcd_group - 1) / xcd_group)
-                              : xcd_group < 0 ? 8 * per_xcd
-                                              : bound * a.num_kv_heads;
-  const int64_t dec_wgs = a.single_query_seqs != 0 ? ((int64_t)a.num_seqs * a.num_kv_heads + 7) / 8 * 8 : 0;
-  if (prefill_wgs + dec_wgs == 0) return hipSuccess;
-  if (prefill_wgs + dec_wgs > 0x7ffffff0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((paged_prefill_kernel<D, NW, QT>), dim3((unsigned)(dec_wgs + prefill_wgs)), dim3(NW * 64), 0,
-                     stream, a, (int)bound, dense_qb, xcd_group, (int)per_xcd, single_query_view(a),
-                     (int)dec_wgs);
+  p.xcd_group = (a.num_kv_heads <= 8 && 8 % a.num_kv_heads == 0) ? 8 / a.num_kv_heads : 0;
+  if (p.dense_qb > 0 && (int64_t)a.num_seqs * a.num_kv_heads >= 64) p.xcd_group = -1;
+  p.per_xcd = (p.bound * a.num_kv_heads + 7) / 8;
+  p.prefill_wgs = p.xcd_group > 0 ? 8 * ((p.bound + p.xcd_group - 1) / p.xcd_group)
+                  : p.xcd_group < 0 ? 8 * p.per_xcd
+                                    : p.bound * a.num_kv_heads;
+  p.dec_wgs = a.single_query_seqs != 0 ? ((int64_t)a.num_seqs * a.num_kv_heads + 7) / 8 * 8 : 0;
+  return p;
+}
+
+template <int D, int NW, int QT>
+static hipError_t launch_prefill(const PrefillArgs& a, const PrefillGrid& p, hipStream_t stream) {
+  if (p.prefill_wgs + p.dec_wgs == 0) return hipSuccess;
+  if (p.prefill_wgs + p.dec_wgs > 0x7ffffff0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((paged_prefill_kernel<D, NW, QT>), dim3((unsigned)(p.dec_wgs + p.prefill_wgs)), dim3(NW * 64),
+                     0, stream, a, (int)p.bound, p.dense_qb, p.xcd_group, (int)p.per_xcd, single_query_view(a),
+                     (int)p.dec_wgs);
   return hipGetLastError();
+}
+
+// Two column tiles per wave (16 query rows per work-group) unless that grid
+// gives fewer than two prefill work-groups per CU (short batches, mixed
+// steps): then one tile per wave, 8 rows per work-group, twice the work-groups
+// (mixed 1 x 512 + 63 decodes: 39.5 -> 34.4 us; 8 x (1024 + 128): 34.7 -> 33.2 us).
+template <int D>
+static hipError_t prefill_for_dim(const PrefillArgs& a, hipStream_t stream) {
+  const int G = a.num_heads / a.num_kv_heads;
+  const PrefillGrid p2 = plan_prefill(a, 4 * 2 * (16 / G));
+  if (p2.prefill_wgs >= 2 * (int64_t)device_cus()) return launch_prefill<D, 4, 2>(a, p2, stream);
+  return launch_prefill<D, 4, 1>(a, plan_prefill(a, 4 * 1 * (16 / G)), stream);
 }
 
 hipError_t paged_prefill(const PrefillArgs& a, hipStream_t stream) {
   switch (a.head_dim) {
-    case 64: return launch_prefill<64, 4, 2>(a, stream);
-    case 128: return launch_prefill<128, 4, 2>(a, stream);
+    case 64: return prefill_for_dim<64>(a, stream);
+    case 128: return prefill_for_dim<128>(a, stream);
     default: return hipErrorInvalidValue;
   }
 }
