@@ -124,6 +124,11 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   // boustrophedon order (0 1 | 1 0 | 0 1 ...): each L2 holds one KV head's
   // keys, and the heavy-to-light run of a sequence's blocks spreads evenly.
   const int id = blockIdx.x - n_dec_wgs;
+  // The arguments that address the metadata and table loads below, read
+  // with the mapping's own: otherwise their wait splits those loads' round trip.
+  asm volatile("" ::"s"(a.block_tables), "s"(a.bt_stride), "s"(a.max_blocks), "s"(a.query_start_loc),
+               "s"(a.seq_lens), "s"(a.context_lens), "s"(a.q), "s"(a.q_st), "s"(a.q_sh), "s"(a.k_cache),
+               "s"(a.v_cache), "s"(a.c_st), "s"(a.c_sh), "s"(a.c_sb), "s"(a.num_pages));
   int kvh, r;
   if (xcd_group < 0) {
     const int L = (id & 7) * per_xcd + (id >> 3);
@@ -150,12 +155,48 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   } else if (!find_query_block(a, QB, r, s, qb)) {
     return;
   }
-  const int q_start = uniform(a.query_start_loc[s]);
-  const int q_len = uniform(a.query_start_loc[s + 1]) - q_start;
+
+  // The sequence's metadata and the page numbers of its first two 64-key
+  // tiles, as scalar loads (constant address space) issued together and
+  // waited for once, above the returns below (a work-group that returns leaves
+  // the entries unused): one round trip. A later tile's entries are fetched a
+  // half step before their use. page_fetch issues the loads of tile kt's four
+  // entries (entries past the row's last are clamped to it: only the last
+  // tiles reach there); page_finish waits for them and forms byte offsets.
+  typedef const int32_t __attribute__((address_space(4)))* ConstI32;
+  int q_start = ((ConstI32)a.query_start_loc)[s];
+  int q_end = ((ConstI32)a.query_start_loc)[s + 1];
+  int seq_len = ((ConstI32)a.seq_lens)[s];
+  int ctx = ((ConstI32)a.context_lens)[s];
+  constexpr int PAGES_PER_TILE = KT / 16;
+  static_assert(PAGES_PER_TILE == 4, "page_finish consumes four entries");
+  const ConstI32 bts = (ConstI32)(a.block_tables + (int64_t)s * a.bt_stride);
+  const uint32_t page_bytes = (uint32_t)a.c_sb * 2u;  // c_sb < 2^31, checked on the host
+  // (No branch between the fast and the clamped form: the waits that close
+  // each side of one would split the loads' round trip.)
+  auto page_fetch = [&](int kt, int (&raw)[PAGES_PER_TILE]) __attribute__((always_inline)) {
+    const int i0 = kt * PAGES_PER_TILE;
+#pragma unroll
+    for (int pg = 0; pg < PAGES_PER_TILE; ++pg) raw[pg] = bts[min(i0 + pg, a.max_blocks - 1)];
+  };
+  auto page_finish = [&](int (&raw)[PAGES_PER_TILE], int64_t (&po)[PAGES_PER_TILE]) __attribute__((always_inline)) {
+    asm volatile("" : "+s"(raw[0]), "+s"(raw[1]), "+s"(raw[2]), "+s"(raw[3]));
+#pragma unroll
+    for (int pg = 0; pg < PAGES_PER_TILE; ++pg)
+      po[pg] = (int64_t)((uint64_t)(uint32_t)min(max(raw[pg], 0), a.num_pages - 1) * page_bytes);
+  };
+  int64_t po_v[PAGES_PER_TILE], po_k[PAGES_PER_TILE];
+  {
+    int raw0[PAGES_PER_TILE], raw1[PAGES_PER_TILE];
+    page_fetch(0, raw0);
+    page_fetch(1, raw1);
+    asm volatile("" : "+s"(q_start), "+s"(q_end), "+s"(seq_len), "+s"(ctx));
+    page_finish(raw0, po_v);
+    page_finish(raw1, po_k);
+  }
+  const int q_len = q_end - q_start;
   if (qb * QB >= q_len) return;
   if (q_len == 1 && a.single_query_seqs != 0) return;  // on the decode work-groups
-  const int seq_len = uniform(a.seq_lens[s]);
-  const int ctx = uniform(a.context_lens[s]);
   const int q_last = min(q_len, (qb + 1) * QB) - 1;
   const int hi = min(seq_len, ctx + q_last + 1);
   const int n_tiles = hi > 0 ? (hi + KT - 1) / KT : 0;
@@ -205,7 +246,6 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
 
   const unsigned char* kc = reinterpret_cast<const unsigned char*>(a.k_cache) + (int64_t)kvh * a.c_sh * 2;
   const unsigned char* vc = reinterpret_cast<const unsigned char*>(a.v_cache) + (int64_t)kvh * a.c_sh * 2;
-  const int32_t* bt = a.block_tables + (int64_t)s * a.bt_stride;
 
   // Staging: direct global -> LDS loads (global_load_lds_dwordx4). One load
   // of a wave moves 64 chunks of 16 B into 1 KB of LDS, lane i to byte 16·i:
@@ -220,7 +260,6 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   // NW·RPB is a multiple of 16, so rt and both source offsets are the same on
   // every tile and every r; the page of block e is r·PG_STEP + (wave offset).
   constexpr int RPB = 1024 / RB;
-  constexpr int PAGES_PER_TILE = KT / 16;
   constexpr int PG_STEP = NW * 64 / (2 * D);
   static_assert(RPB * PER_T * NW == KT, "a tile is PER_T loads per wave");
   static_assert((NW * RPB) % 16 == 0, "row-in-page of a lane is the same for every r");
@@ -235,38 +274,6 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   const uint32_t lds_base = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) unsigned char*)lds);
   const uint32_t lds_wave = lds_base + (uint32_t)w * 1024u;
 
-  // The four page numbers of a tile, as scalar loads (constant address space)
-  // issued together and consumed together: one wait for all four. Entries
-  // past the row's last table entry are clamped to it (only the last tiles
-  // reach there).
-  typedef const int32_t __attribute__((address_space(4)))* ConstI32;
-  const ConstI32 bts = (ConstI32)bt;
-  const uint32_t page_bytes = (uint32_t)a.c_sb * 2u;  // c_sb < 2^31, checked on the host
-  // page_fetch issues the scalar loads of tile kt's entries; page_finish
-  // waits for them (one wait for all four) and forms the byte offsets. A
-  // fetch issued a half step before its finish hides the load latency.
-  auto page_fetch = [&](int kt, int (&raw)[PAGES_PER_TILE]) __attribute__((always_inline)) {
-    const int i0 = kt * PAGES_PER_TILE;
-    if (i0 + PAGES_PER_TILE <= a.max_blocks) {
-#pragma unroll
-      for (int pg = 0; pg < PAGES_PER_TILE; ++pg) raw[pg] = bts[i0 + pg];
-    } else {
-#pragma unroll
-      for (int pg = 0; pg < PAGES_PER_TILE; ++pg) raw[pg] = bts[min(i0 + pg, a.max_blocks - 1)];
-    }
-  };
-  auto page_finish = [&](int (&raw)[PAGES_PER_TILE], int64_t (&po)[PAGES_PER_TILE]) __attribute__((always_inline)) {
-    asm volatile("" : "+s"(raw[0]), "+s"(raw[1]), "+s"(raw[2]), "+s"(raw[3]));
-#pragma unroll
-    for (int pg = 0; pg < PAGES_PER_TILE; ++pg)
-      po[pg] = (int64_t)((uint64_t)(uint32_t)min(max(raw[pg], 0), a.num_pages - 1) * page_bytes);
-  };
-  auto page_bases = [&](int kt, int64_t (&po)[PAGES_PER_TILE]) __attribute__((always_inline)) {
-    int raw[PAGES_PER_TILE];
-    page_fetch(kt, raw);
-    page_finish(raw, po);
-  };
-  static_assert(PAGES_PER_TILE == 4, "page_bases consumes four entries");
 
   // The loads are inline asm, invisible to the compiler's wait insertion
   // (which would otherwise wait for them before every LDS read); each wave
@@ -437,7 +444,10 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   // Half x = 2j + h is keys 32x .. 32x+31 (tile j, half h). Half step x
   // computes Sᵀ(x+1) while forming P(x) from Sᵀ(x), rescales acc, masks
   // Sᵀ(x+1) if needed, then accumulates PV(x) while taking the max of Sᵀ(x+1).
-  // Buffers: K(j) in K buffer j&1, V(j) in V buffer j&1. Per tile j:
+  // Buffers: K(j) in K buffer j&1, V(j) in V buffer j&1.
+  // A work-group with at most two tiles (short) loads all of them in the
+  // prologue and then runs its halves with no loads, waits or barriers.
+  // Otherwise the prologue loads K(0), V(0), K(1), and per tile j:
   //   start:  loads of V(j+1) into V buffer (j+1)&1 (V(j-1) is consumed);
   //   half 0: reads K(j) (its second half) and V(j);
   //   mid:    waits for K(j+1) (loaded since the previous mid), barrier —
@@ -445,17 +455,19 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   //           loads K(j+2) into K buffer j&1;
   //   half 1: reads K(j+1) (its first half) and V(j);
   //   end:    waits for V(j+1), clears its rows past hi, barrier.
-  // Loads are waited for in issue order (vmcnt), one tile step after issue.
-  int64_t po_v[PAGES_PER_TILE], po_k[PAGES_PER_TILE];
+  // Loads are waited for in issue order (vmcnt), one tile step after issue;
+  // the last steps load tiles past n_tiles (clamped table entries, in bounds)
+  // that are never read, so the steady state has no branches around loads.
+  const bool short_wg = n_tiles <= 2;
   f32x4_t S0[QT][2], S1[QT][2];
   if (n_tiles > 0) {
-    page_bases(0, po_v);
     stage_k(po_v, 0);
     stage_v(po_v, 0);
-    page_bases(1, po_k);
-    stage_k(po_k, 1);
+    if (n_tiles > 1 || !short_wg) stage_k(po_k, 1);
+    if (n_tiles == 2) stage_v(po_k, 1);
     wait_loads();
     zero_v_tail(0, 0);
+    if (n_tiles == 2) zero_v_tail(1, 1);
 #pragma unroll
     for (int pg = 0; pg < PAGES_PER_TILE; ++pg) po_v[pg] = po_k[pg];
   }
@@ -505,7 +517,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   };
   auto wait_older_loads = [&]() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_T) : "memory"); };
   // po_v holds the pages of tile j+1 (staged for K(j+1) at the previous mid
-  // step) when step j starts.
+  // step or in the prologue) when step j starts.
   auto tile_step = [&](const int j, const int b) __attribute__((always_inline)) {  // b = j & 1
     int raw[PAGES_PER_TILE];
     page_fetch(j + 2, raw);
@@ -522,14 +534,23 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
 #pragma unroll
     for (int pg = 0; pg < PAGES_PER_TILE; ++pg) po_v[pg] = po_k[pg];
   };
-  // Two tiles per iteration, so that buffer numbers are constants.
-  for (int j = 0; j < n_tiles; j += 2) {
-    tile_step(j, 0);
-    if (j + 1 < n_tiles) tile_step(j + 1, 1);
+  if (short_wg) {
+    // Every tile is in LDS; the last half's Sᵀ(x+1) reads K buffer 0 (in
+    // bounds, never used).
+    half_step(0, S0, S1, 0, 1, 0, 0);
+    half_step(1, S1, S0, 1, 0, 0, 1);
+    half_step(2, S0, S1, 1, 1, 1, 0);
+    half_step(3, S1, S0, 0, 0, 1, 1);
+  } else {
+    // Two tiles per iteration, so that buffer numbers are constants.
+    for (int j = 0; j < n_tiles; j += 2) {
+      tile_step(j, 0);
+      if (j + 1 < n_tiles) tile_step(j + 1, 1);
+    }
+    // The last step's prefetch into LDS is still in flight: it must land
+    // before the work-group ends and its LDS is handed to another.
+    wait_loads();
   }
-  // The last step's prefetch into LDS is still in flight: it must land
-  // before the work-group ends and its LDS is handed to another.
-  wait_loads();
 
 #pragma unroll
   for (int ct = 0; ct < QT; ++ct) {
