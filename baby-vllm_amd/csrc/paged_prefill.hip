@@ -4,11 +4,12 @@
 //
 // Replaces paged_prefill_attn_kernel (babyvllm/kernels/paged_prefill.py:6-101).
 //
-// Work-group = (sequence, KV head, block of QB query rows). All G query heads
-// of the KV head are packed into the MFMA column dimension, so every K/V tile
-// is staged once per work-group and shared by the whole GQA group:
-//   column n of a 16-column tile = (query n / G, head n % G), n < (16 / G)·G.
-// Each of the NW waves owns QT such column tiles; QB = NW·QT·(16/G).
+// Work-group = (sequence, KV head, block of CB columns). The columns are the
+// sequence's (query, head) pairs of the KV head's G query heads, numbered
+// query-major (f = query·G + head), so every K/V tile is staged once per
+// work-group and shared by the whole GQA group, and every MFMA column holds a
+// pair whatever G is (a 16-column tile may span queries: the causal limit is
+// per column). Each of the NW waves owns QT 16-column tiles; CB = NW·QT·16.
 // Keys come in tiles of 64 (four 16-token pages), moved from the cache into LDS
 // by direct global->LDS loads (no staging registers), rows XOR-swizzled instead
 // of padded. K and V each have two LDS buffers; K runs one tile ahead of V.
@@ -36,12 +37,14 @@
 
 namespace bvllm {
 
-// Query blocks of QB rows are numbered sequence by sequence, the blocks of a
-// sequence last (most keys) first; a sequence with one query token has none
-// when the decode work-groups compute it. Finds the sequence s and block qb of
-// number r, or returns false if r is past the last block. Every wave computes
-// the same wave-uniform answer (a scan of the per-sequence block counts).
-__device__ __forceinline__ bool find_query_block(const PrefillArgs& a, int QB, int r, int& s_out, int& qb_out) {
+// Blocks of CB columns (a sequence's q_len·G (query, head) pairs, numbered
+// query-major) are numbered sequence by sequence, the blocks of a sequence last
+// (most keys) first; a sequence with one query token has none when the decode
+// work-groups compute it. Finds the sequence s and block qb of number r, or
+// returns false if r is past the last block. Every wave computes the same
+// wave-uniform answer (a scan of the per-sequence block counts).
+__device__ __forceinline__ bool find_query_block(const PrefillArgs& a, int CB, int r, int& s_out, int& qb_out) {
+  const int G = a.num_heads / a.num_kv_heads;
   constexpr int kChunk = 4;  // 64-sequence slices whose counts are loaded together
   const int lane = lane_id();
   int before = 0;
@@ -53,7 +56,7 @@ __device__ __forceinline__ bool find_query_block(const PrefillArgs& a, int QB, i
       nb[c] = 0;
       if (s < a.num_seqs) {
         const int ql = a.query_start_loc[s + 1] - a.query_start_loc[s];
-        nb[c] = (ql == 1 && a.single_query_seqs != 0) ? 0 : (ql + QB - 1) / QB;
+        nb[c] = (ql == 1 && a.single_query_seqs != 0) ? 0 : (ql * G + CB - 1) / CB;
       }
     }
 #pragma unroll
@@ -112,8 +115,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   }
 
   const int G = a.num_heads / a.num_kv_heads;
-  const int QP = 16 / G;
-  const int QB = NW * QT * QP;
+  constexpr int CB = NW * QT * 16;  // columns of a work-group's block
 
   // Work-groups are dispatched round-robin over the 8 XCDs (XCD = id mod 8).
   // xcd_group == -1 (many (sequence, KV head) pairs, dense numbering): each XCD
@@ -152,7 +154,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
     // Dense numbering: every sequence owns dense_qb block numbers.
     s = r / dense_qb;
     qb = dense_qb - 1 - (r - s * dense_qb);
-  } else if (!find_query_block(a, QB, r, s, qb)) {
+  } else if (!find_query_block(a, CB, r, s, qb)) {
     return;
   }
 
@@ -195,9 +197,10 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
     page_finish(raw1, po_k);
   }
   const int q_len = q_end - q_start;
-  if (qb * QB >= q_len) return;
+  const int n_cols = q_len * G;
+  if (qb * CB >= n_cols) return;
   if (q_len == 1 && a.single_query_seqs != 0) return;  // on the decode work-groups
-  const int q_last = min(q_len, (qb + 1) * QB) - 1;
+  const int q_last = (min(n_cols, (qb + 1) * CB) - 1) / G;
   const int hi = min(seq_len, ctx + q_last + 1);
   const int n_tiles = hi > 0 ? (hi + KT - 1) / KT : 0;
 
@@ -205,25 +208,27 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   const int n = lane & 15;
   const int g = lane >> 4;
   const int w = wave_id();
-  const int qi_in = n / G;
-  const int hl = n - qi_in * G;
-  const bool col_ok = n < QP * G;
 
-  const int wave_q0 = qb * QB + w * QT * QP;  // first query index of this wave
-  const bool wave_live = wave_q0 < q_len;
-  const int wave_hi = ctx + min(q_len - 1, wave_q0 + QT * QP - 1);  // last visible key position
+  // The wave's columns: f = wave_f0 + 16·ct + n of the block's flat
+  // (query, head) numbering, query f / G and head f mod G.
+  const int wave_f0 = qb * CB + w * QT * 16;
+  const int wave_q0 = wave_f0 / G;  // first query index of this wave
+  const bool wave_live = wave_f0 < n_cols;
+  const int wave_hi = ctx + min(q_len - 1, (wave_f0 + QT * 16 - 1) / G);  // last visible key position
 
-  int qi[QT];
+  int qi[QT], hl[QT];
   int qpos[QT];
   bool valid[QT];
   uint4 qreg[QT][KC];
 #pragma unroll
   for (int ct = 0; ct < QT; ++ct) {
-    qi[ct] = wave_q0 + ct * QP + qi_in;
-    valid[ct] = col_ok && qi[ct] < q_len;
+    const int f = wave_f0 + 16 * ct + n;
+    qi[ct] = f / G;
+    hl[ct] = f - qi[ct] * G;
+    valid[ct] = f < n_cols;
     qpos[ct] = valid[ct] ? ctx + qi[ct] : 0x7fffffff;
     const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)(q_start + qi[ct]) * a.q_st +
-                           (int64_t)(kvh * G + hl) * a.q_sh;
+                           (int64_t)(kvh * G + hl[ct]) * a.q_sh;
 #pragma unroll
     for (int c = 0; c < KC; ++c)
       qreg[ct][c] = valid[ct] ? ld16(qrow + 8 * (4 * c + g)) : make_uint4(0, 0, 0, 0);
@@ -559,7 +564,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     // acc[ct][c][i] is dim 16c + 4g + i.
     uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + (int64_t)(q_start + qi[ct]) * a.o_st +
-                     (int64_t)(kvh * G + hl) * a.o_sh + 4 * g;
+                     (int64_t)(kvh * G + hl[ct]) * a.o_sh + 4 * g;
 #pragma unroll
     for (int c = 0; c < VD; ++c) {
       uint2 pk;
@@ -591,7 +596,8 @@ static DecodeArgs single_query_view(const PrefillArgs& p) {
   return a;
 }
 
-// Launch geometry of a prefill batch for QB query rows per work-group.
+// Launch geometry of a prefill batch for CB columns ((query, head) pairs of
+// one KV head) per work-group.
 struct PrefillGrid {
   int64_t bound = 0;  // query-block numbers
   int dense_qb = 0;   // > 0: dense numbering with this many blocks per sequence
@@ -600,20 +606,21 @@ struct PrefillGrid {
   int64_t prefill_wgs = 0, dec_wgs = 0;
 };
 
-static PrefillGrid plan_prefill(const PrefillArgs& a, int64_t QB) {
+static PrefillGrid plan_prefill(const PrefillArgs& a, int64_t CB) {
   PrefillGrid p;
-  // Upper bound of the query-block count: Σ ceil(q_s / QB) ≤ (T + S·(QB-1)) / QB
+  const int64_t G = a.num_heads / a.num_kv_heads;
+  // Upper bound of the block count: Σ ceil(G·q_s / CB) ≤ (G·T + S·(CB-1)) / CB
   // over the sequences the prefill work-groups compute.
   int64_t T = a.num_tokens, S = a.num_seqs;
   if (a.single_query_seqs > 0) {
     T -= a.single_query_seqs;
     S -= a.single_query_seqs;
   }
-  p.bound = S > 0 ? (T + S * (QB - 1)) / QB : 0;
-  // Query blocks are numbered densely (ceil(max_query_len / QB) per sequence,
+  p.bound = S > 0 ? (G * T + S * (CB - 1)) / CB : 0;
+  // Blocks are numbered densely (ceil(G·max_query_len / CB) per sequence,
   // found by division) unless that wastes more than a quarter of the grid on
   // empty blocks, as in a mixed step; then compactly (found by a scan).
-  const int64_t dense = (a.max_query_len + QB - 1) / QB;
+  const int64_t dense = (G * a.max_query_len + CB - 1) / CB;
   if (dense * a.num_seqs * 4 <= p.bound * 5) {
     p.dense_qb = (int)dense;
     p.bound = dense * a.num_seqs;
@@ -638,16 +645,16 @@ static hipError_t launch_prefill(const PrefillArgs& a, const PrefillGrid& p, hip
   return hipGetLastError();
 }
 
-// Two column tiles per wave (16 query rows per work-group) unless that grid
+// Two column tiles per wave (128 columns per work-group) unless that grid
 // gives fewer than two prefill work-groups per CU (short batches, mixed
-// steps): then one tile per wave, 8 rows per work-group, twice the work-groups
-// (mixed 1 x 512 + 63 decodes: 39.5 -> 34.4 us; 8 x (1024 + 128): 34.7 -> 33.2 us).
+// steps): then one tile per wave, 64 columns per work-group, twice the
+// work-groups (mixed 1 x 512 + 63 decodes: 39.5 -> 34.4 us; 8 x (1024 + 128):
+// 34.7 -> 33.2 us).
 template <int D>
 static hipError_t prefill_for_dim(const PrefillArgs& a, hipStream_t stream) {
-  const int G = a.num_heads / a.num_kv_heads;
-  const PrefillGrid p2 = plan_prefill(a, 4 * 2 * (16 / G));
+  const PrefillGrid p2 = plan_prefill(a, 4 * 2 * 16);
   if (p2.prefill_wgs >= 2 * (int64_t)device_cus()) return launch_prefill<D, 4, 2>(a, p2, stream);
-  return launch_prefill<D, 4, 1>(a, plan_prefill(a, 4 * 1 * (16 / G)), stream);
+  return launch_prefill<D, 4, 1>(a, plan_prefill(a, 4 * 1 * 16), stream);
 }
 
 hipError_t paged_prefill(const PrefillArgs& a, hipStream_t stream) {

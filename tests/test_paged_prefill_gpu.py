@@ -177,8 +177,11 @@ def test_many_sequences_of_mixed_lengths(n_seqs):
     assert_attn_close(actual, _oracle(q, kv_cache, md, 7))
 
 
-@pytest.mark.parametrize("hkv,group,d", [(8, 2, 128), (1, 8, 128), (3, 2, 64), (16, 1, 64)])
+@pytest.mark.parametrize("hkv,group,d", [(8, 2, 128), (1, 8, 128), (3, 2, 64), (16, 1, 64),
+                                         (2, 3, 128), (1, 5, 64), (2, 6, 128), (1, 16, 64)])
 def test_kv_head_counts_and_xcd_groups(hkv, group, d):
+    """Group sizes that do not divide 16 put the heads of one query in two
+    16-column tiles (and the queries of one tile in two work-groups)."""
     specs = [(0, 70), (130, 1), (33, 45), (7, 1), (0, 16)]
     q, kv_cache, md = build_prefill_case(specs, hkv, group, d, seed=hkv)
     actual = _kernel()(q, kv_cache, md, d ** -0.5)
