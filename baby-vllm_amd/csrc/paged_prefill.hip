@@ -17,11 +17,11 @@
 //   Sᵀ[16 keys × 16 cols] = K · Qᵀ       (K operand from LDS)
 //   Oᵀ[D × 16 cols]      += Vᵀ · Pᵀ      (Pᵀ from the Sᵀ registers, Vᵀ by LDS
 //                                         transpose reads)
-// software-pipelined by half: Sᵀ of the next half is computed while P and the
-// max of the current half are formed, so MFMA and VALU work of one wave
-// overlap. P uses the running max as its reference; only when a half's max
-// exceeds it by more than 8 (log2 units) is the max raised and P formed
-// again, so the max never delays P. The row sums come from an MFMA of P with
+// software-pipelined by half: Sᵀ of the next half is computed while P of the
+// current half is formed, so MFMA and VALU work of one wave overlap. P uses
+// the running max as its reference; only when some P exceeds 2^8 (a score
+// above the reference by more than 8 in log2 units) is the max raised and P
+// formed again, so the max never delays P. The row sums come from an MFMA of P with
 // an all-ones operand, next to the PV product.
 // Keys at or past hi = min(seq_len, ctx + last query + 1) are masked, and their
 // V rows are zeroed in LDS, so cache slots that were never written (possibly
@@ -371,24 +371,30 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   // The scores' max of each column over a half, in log2 units (the scale is
   // > 0, so it commutes with the max): a chain of three-input maxima, then
   // across the four lane groups.
+  auto half_max1 = [&](const f32x4_t (&S)[QT][2], const int ct) __attribute__((always_inline)) -> float {
+    float mx = fmax_prop(fmax_prop(S[ct][0][0], S[ct][0][1]), S[ct][0][2]);
+    mx = fmax_prop(fmax_prop(mx, S[ct][0][3]), S[ct][1][0]);
+    mx = fmax_prop(fmax_prop(mx, S[ct][1][1]), S[ct][1][2]);
+    mx = fmax_prop(mx, S[ct][1][3]);
+    return max_across_groups(mx) * a.scale_log2;
+  };
   auto half_max = [&](const f32x4_t (&S)[QT][2], float (&mt)[QT]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int ct = 0; ct < QT; ++ct) {
-      float mx = fmax_prop(fmax_prop(S[ct][0][0], S[ct][0][1]), S[ct][0][2]);
-      mx = fmax_prop(fmax_prop(mx, S[ct][0][3]), S[ct][1][0]);
-      mx = fmax_prop(fmax_prop(mx, S[ct][1][1]), S[ct][1][2]);
-      mx = fmax_prop(mx, S[ct][1][3]);
-      mt[ct] = max_across_groups(mx) * a.scale_log2;
-    }
+    for (int ct = 0; ct < QT; ++ct) mt[ct] = half_max1(S, ct);
   };
   // P = 2^(s·scale − m), packed to bf16 as the B operand of the PV product
   // over the half's 32 keys.
+  float pmax[QT];  // the lane's largest P of the half, per column tile
   auto softmax_p1 = [&](const f32x4_t (&S)[QT][2], uint4 (&pb)[QT], const int ct) __attribute__((always_inline)) {
     float p[2][4];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) p[t][i] = fast_exp2(__builtin_fmaf(S[ct][t][i], a.scale_log2, -m[ct]));
+    float px = fmax_prop(fmax_prop(p[0][0], p[0][1]), p[0][2]);
+    px = fmax_prop(fmax_prop(px, p[0][3]), p[1][0]);
+    px = fmax_prop(fmax_prop(px, p[1][1]), p[1][2]);
+    pmax[ct] = fmax_prop(px, p[1][3]);
     pb[ct].x = pack_bf16x2_hw(p[0][0], p[0][1]);
     pb[ct].y = pack_bf16x2_hw(p[0][2], p[0][3]);
     pb[ct].z = pack_bf16x2_hw(p[1][0], p[1][1]);
@@ -402,13 +408,16 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   // only when some column's new max exceeds it by more than 8 (a factor 256;
   // P stays far inside fp32 and bf16 range, and the final division by the
   // row sum removes the common factor): then acc and the row sums are
-  // rescaled by 2^(m_old − m_new) and P is formed again. So P does not wait
-  // for the max, which is computed alongside it and only gates this rare path.
-  auto raise_max = [&](const f32x4_t (&S)[QT][2], const float (&mt)[QT], uint4 (&pb)[QT]) __attribute__((always_inline)) {
+  // rescaled by 2^(m_old − m_new) and P is formed again. That happens exactly
+  // when some P of the column exceeds 2^8, so each lane tests the largest of
+  // its own P (formed anyway), a ballot joins the lanes, and only on this rare
+  // path is the column max itself formed: P never waits for a max, and the
+  // common path has no cross-lane reduction.
+  auto raise_max = [&](const f32x4_t (&S)[QT][2], uint4 (&pb)[QT]) __attribute__((always_inline)) {
 #pragma unroll
     for (int ct = 0; ct < QT; ++ct) {
-      if (__builtin_amdgcn_ballot_w64(!(mt[ct] <= m[ct] + 8.0f)) != 0) {
-        const float m_new = fmax_prop(m[ct], mt[ct]);
+      if (__builtin_amdgcn_ballot_w64(!(pmax[ct] <= 256.0f)) != 0) {
+        const float m_new = fmax_prop(m[ct], half_max1(S, ct));
         const float alpha = fast_exp2(m[ct] - m_new);
         m[ct] = m_new;
 #pragma unroll
@@ -503,17 +512,15 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
     // accumulators have a single definition per step.
     uint4 pb[QT];
     if (x < wave_halves) {
-      float mt[QT];
       __builtin_amdgcn_s_setprio(1);
       qk(Sn, kbuf_next, h_next);
       softmax_p(Sc, pb);
-      half_max(Sc, mt);
       // P is formed here, under the QKᵀ MFMAs and beside the max, not sunk
       // past the branches below.
 #pragma unroll
       for (int ct = 0; ct < QT; ++ct) asm volatile("" ::"v"(pb[ct].x), "v"(pb[ct].y), "v"(pb[ct].z), "v"(pb[ct].w));
       __builtin_amdgcn_s_setprio(0);
-      raise_max(Sc, mt, pb);
+      raise_max(Sc, pb);
       if (needs_mask(32 * (x + 1))) mask(Sn, 32 * (x + 1));
       __builtin_amdgcn_s_setprio(1);
       pv(pb, vbuf, h);

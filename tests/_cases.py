@@ -88,6 +88,23 @@ def build_prefill_case(specs, hkv, group, d, seed=0, nan_fill=True, device="cuda
     return q, kv_cache, md
 
 
+def scale_keys_by_position(kv_cache, block_tables, seq_lens, factor):
+    """Multiplies the key at position p of every row by factor(p), in place:
+    with growing factors a row's later scores exceed its running max many
+    times over, which drives the kernels' rescale paths."""
+    bs = kv_cache.shape[2]
+    bt = block_tables.cpu()
+    for row, n in enumerate(int(x) for x in seq_lens):
+        if n == 0:
+            continue
+        pos = torch.arange(n)
+        blocks = bt[row, pos // bs].long().to(kv_cache.device)
+        offs = (pos % bs).to(kv_cache.device)
+        f = torch.tensor([factor(int(p)) for p in pos], dtype=torch.float32, device=kv_cache.device)
+        k = kv_cache[0, blocks, offs].float() * f[:, None, None]
+        kv_cache[0, blocks, offs] = k.to(kv_cache.dtype)
+
+
 def md_to_cpu(md):
     return AttentionMetadata(
         slot_mapping=md.slot_mapping.cpu(), block_tables=md.block_tables.cpu(),

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from oracle import attention as oa
-from tests._cases import BLOCK_SIZE, assert_attn_close, cdiv, make_decode_inputs
+from tests._cases import BLOCK_SIZE, assert_attn_close, cdiv, make_decode_inputs, scale_keys_by_position
 
 pytestmark = [
     pytest.mark.gpu,
@@ -258,3 +258,15 @@ def test_split_per_wave_other_head_configs(hkv, group, d, monkeypatch):
     scale = d ** -0.5
     out = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=2048, partition_blocks=4)
     assert_attn_close(out, _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
+
+
+@pytest.mark.parametrize("partition", [0, 1, 4])
+def test_scores_rising_along_the_row(partition):
+    """Key norms growing with position: the running max of every split is
+    raised page after page (the online-softmax rescale path)."""
+    scale = HEAD_DIM ** -0.5
+    lens = [3000, 1, 700, 0, 2048]
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, width=GRAPH_TABLE_WIDTH + 60, seed=3)
+    scale_keys_by_position(kv_cache, bt, lens, lambda p: 1.0 + p / 64.0)
+    actual = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=3000, partition_blocks=partition)
+    assert_attn_close(actual, _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from oracle import attention as oa
-from tests._cases import assert_attn_close, build_prefill_case, md_to_cpu
+from tests._cases import assert_attn_close, build_prefill_case, md_to_cpu, scale_keys_by_position
 
 pytestmark = [
     pytest.mark.gpu,
@@ -184,5 +184,19 @@ def test_kv_head_counts_and_xcd_groups(hkv, group, d):
     16-column tiles (and the queries of one tile in two work-groups)."""
     specs = [(0, 70), (130, 1), (33, 45), (7, 1), (0, 16)]
     q, kv_cache, md = build_prefill_case(specs, hkv, group, d, seed=hkv)
+    actual = _kernel()(q, kv_cache, md, d ** -0.5)
+    assert_attn_close(actual, _oracle(q, kv_cache, md, group))
+
+
+@pytest.mark.parametrize("growth", [128.0, 24.0])
+@pytest.mark.parametrize("hkv,group,d", [(4, 7, 128), (2, 7, 64)])
+def test_scores_rising_along_the_sequence(growth, hkv, group, d):
+    """Key norms growing with position (factor 1 + p / growth): each row's
+    scores keep exceeding the running max by more than 8 in log2 units, so the
+    kernel raises its max, rescales its accumulators and forms P again many
+    times; growth 24 makes the softmax nearly one-hot at the far end."""
+    specs = [(0, 300), (500, 200), (37, 1), (1000, 64), (0, 5)]
+    q, kv_cache, md = build_prefill_case(specs, hkv, group, d, seed=11)
+    scale_keys_by_position(kv_cache, md.block_tables, md.seq_lens_cpu, lambda p: 1.0 + p / growth)
     actual = _kernel()(q, kv_cache, md, d ** -0.5)
     assert_attn_close(actual, _oracle(q, kv_cache, md, group))
