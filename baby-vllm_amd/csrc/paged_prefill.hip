@@ -35,6 +35,8 @@
 #include "bvllm_abi_internal.h"
 #include "paged_decode_wg.h"
 
+#include <stdlib.h>
+
 namespace bvllm {
 
 // Blocks of CB columns (a sequence's q_len·G (query, head) pairs, numbered
@@ -86,10 +88,12 @@ __device__ __forceinline__ bool find_query_block(const PrefillArgs& a, int CB, i
 constexpr int kDecodeWaves = 4;
 constexpr int kDecodeDepth = 2;
 
-template <int D, int NW, int QT>
+// MB: groups of several blocks per work-group, launched only when every
+// sequence's keys fit two 64-key tiles (the kernel has no streaming path then).
+template <int D, int NW, int QT, bool MB>
 __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a, int n_blocks_bound, int dense_qb,
                                                                   int xcd_group, int per_xcd, DecodeArgs dec,
-                                                                  int n_dec_wgs) {
+                                                                  int n_dec_wgs, int bpw) {
   constexpr int KT = 64;
   constexpr int RB = 2 * D;   // bytes of one key row of K or V (no padding)
   constexpr int TB = 64 * RB;  // bytes of one 64-key K or V tile
@@ -154,7 +158,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
     // Dense numbering: every sequence owns dense_qb block numbers.
     s = r / dense_qb;
     qb = dense_qb - 1 - (r - s * dense_qb);
-  } else if (!find_query_block(a, CB, r, s, qb)) {
+  } else if (!find_query_block(a, CB * (MB ? bpw : 1), r, s, qb)) {
     return;
   }
 
@@ -198,20 +202,33 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   }
   const int q_len = q_end - q_start;
   const int n_cols = q_len * G;
-  if (qb * CB >= n_cols) return;
+  // qb numbers groups of nbpw blocks of CB columns (one block unless MB); the
+  // work-group computes the group's blocks one after another, the last (most
+  // keys) first. Every block of an MB group reads the same (at most two)
+  // tiles: they are staged once, and the later blocks only load their Q.
+  const int nbpw = MB ? bpw : 1;
+  if (qb * nbpw * CB >= n_cols) return;
   if (q_len == 1 && a.single_query_seqs != 0) return;  // on the decode work-groups
-  const int q_last = (min(n_cols, (qb + 1) * CB) - 1) / G;
-  const int hi = min(seq_len, ctx + q_last + 1);
-  const int n_tiles = hi > 0 ? (hi + KT - 1) / KT : 0;
+  const int b_first = qb * nbpw;
+  const int b_last = min(b_first + nbpw, (n_cols + CB - 1) / CB) - 1;
 
   const int lane = lane_id();
   const int n = lane & 15;
   const int g = lane >> 4;
   const int w = wave_id();
 
+  bool kv_staged = false;
+  int blk = b_last;
+  do {  // blocks of the group (a single pass unless MB)
+  const int q_last = (min(n_cols, (blk + 1) * CB) - 1) / G;
+  // (MB: the host checked that no sequence has more than two tiles' pages;
+  // the clamp keeps an inconsistent seq_lens inside the staged tiles.)
+  const int hi = min(min(seq_len, ctx + q_last + 1), MB ? 2 * KT : 0x7fffffff);
+  const int n_tiles = hi > 0 ? (hi + KT - 1) / KT : 0;
+
   // The wave's columns: f = wave_f0 + 16·ct + n of the block's flat
   // (query, head) numbering, query f / G and head f mod G.
-  const int wave_f0 = qb * CB + w * QT * 16;
+  const int wave_f0 = blk * CB + w * QT * 16;
   const int wave_q0 = wave_f0 / G;  // first query index of this wave
   const bool wave_live = wave_f0 < n_cols;
   const int wave_hi = ctx + min(q_len - 1, (wave_f0 + QT * 16 - 1) / G);  // last visible key position
@@ -472,9 +489,9 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   // Loads are waited for in issue order (vmcnt), one tile step after issue;
   // the last steps load tiles past n_tiles (clamped table entries, in bounds)
   // that are never read, so the steady state has no branches around loads.
-  const bool short_wg = n_tiles <= 2;
+  const bool short_wg = MB || n_tiles <= 2;
   f32x4_t S0[QT][2], S1[QT][2];
-  if (n_tiles > 0) {
+  if (n_tiles > 0 && !(kv_staged && short_wg)) {
     stage_k(po_v, 0);
     stage_v(po_v, 0);
     if (n_tiles > 1 || !short_wg) stage_k(po_k, 1);
@@ -485,6 +502,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
 #pragma unroll
     for (int pg = 0; pg < PAGES_PER_TILE; ++pg) po_v[pg] = po_k[pg];
   }
+  kv_staged = short_wg;
   // The Q loads complete here, once, after the first tiles' table fetch and
   // loads were issued behind them: otherwise they look pending at the key
   // loop's header and the compiler drains every load there on each iteration.
@@ -580,6 +598,8 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
       st8(orow + 16 * c, pk);
     }
   }
+  if (!MB) break;
+  } while (--blk >= b_first);
 }
 
 // Decode view of a prefill batch: row b is sequence b; the decode work-group
@@ -643,13 +663,39 @@ static PrefillGrid plan_prefill(const PrefillArgs& a, int64_t CB) {
 }
 
 template <int D, int NW, int QT>
-static hipError_t launch_prefill(const PrefillArgs& a, const PrefillGrid& p, hipStream_t stream) {
+static hipError_t launch_prefill(const PrefillArgs& a, const PrefillGrid& p, int bpw, hipStream_t stream) {
   if (p.prefill_wgs + p.dec_wgs == 0) return hipSuccess;
   if (p.prefill_wgs + p.dec_wgs > 0x7ffffff0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((paged_prefill_kernel<D, NW, QT>), dim3((unsigned)(p.dec_wgs + p.prefill_wgs)), dim3(NW * 64),
-                     0, stream, a, (int)p.bound, p.dense_qb, p.xcd_group, (int)p.per_xcd, single_query_view(a),
-                     (int)p.dec_wgs);
+  if (bpw > 1)
+    hipLaunchKernelGGL((paged_prefill_kernel<D, NW, QT, true>), dim3((unsigned)(p.dec_wgs + p.prefill_wgs)),
+                       dim3(NW * 64), 0, stream, a, (int)p.bound, p.dense_qb, p.xcd_group, (int)p.per_xcd,
+                       single_query_view(a), (int)p.dec_wgs, bpw);
+  else
+    hipLaunchKernelGGL((paged_prefill_kernel<D, NW, QT, false>), dim3((unsigned)(p.dec_wgs + p.prefill_wgs)),
+                       dim3(NW * 64), 0, stream, a, (int)p.bound, p.dense_qb, p.xcd_group, (int)p.per_xcd,
+                       single_query_view(a), (int)p.dec_wgs, 1);
   return hipGetLastError();
+}
+
+// Blocks per work-group: when every sequence's keys fit two 64-key tiles
+// (table width ≤ 8 pages) and the one-block grid is more than one round of
+// two work-groups per CU, a work-group takes several blocks of one (sequence,
+// KV head), which read the same tiles: the fewest per work-group that make
+// the grid one round (64 x 128: 4 blocks per work-group, 512 work-groups).
+// BVLLM_PREFILL_BLOCKS_PER_WG overrides the choice when the table width allows
+// it (read per launch: tests vary it).
+static int prefill_blocks_per_wg(const PrefillArgs& a, const PrefillGrid& p1) {
+  if (a.max_blocks > 8) return 1;
+  const char* env = getenv("BVLLM_PREFILL_BLOCKS_PER_WG");
+  const int forced = env ? atoi(env) : 0;
+  if (forced > 0) return forced;
+  if (p1.dense_qb <= 1) return 1;
+  const int64_t slots = 2 * (int64_t)device_cus();
+  const int64_t pairs = (int64_t)a.num_seqs * a.num_kv_heads;
+  const int64_t per_pair = slots / pairs;  // work-groups per (sequence, KV head) in one round
+  if (per_pair >= p1.dense_qb) return 1;
+  if (per_pair == 0) return p1.dense_qb;
+  return (int)((p1.dense_qb + per_pair - 1) / per_pair);
 }
 
 // Two column tiles per wave (128 columns per work-group) unless that grid
@@ -660,8 +706,12 @@ static hipError_t launch_prefill(const PrefillArgs& a, const PrefillGrid& p, hip
 template <int D>
 static hipError_t prefill_for_dim(const PrefillArgs& a, hipStream_t stream) {
   const PrefillGrid p2 = plan_prefill(a, 4 * 2 * 16);
-  if (p2.prefill_wgs >= 2 * (int64_t)device_cus()) return launch_prefill<D, 4, 2>(a, p2, stream);
-  return launch_prefill<D, 4, 1>(a, plan_prefill(a, 4 * 1 * 16), stream);
+  if (p2.prefill_wgs >= 2 * (int64_t)device_cus()) {
+    const int bpw = prefill_blocks_per_wg(a, p2);
+    if (bpw == 1) return launch_prefill<D, 4, 2>(a, p2, 1, stream);
+    return launch_prefill<D, 4, 2>(a, plan_prefill(a, 4 * 2 * 16 * (int64_t)bpw), bpw, stream);
+  }
+  return launch_prefill<D, 4, 1>(a, plan_prefill(a, 4 * 1 * 16), 1, stream);
 }
 
 hipError_t paged_prefill(const PrefillArgs& a, hipStream_t stream) {
