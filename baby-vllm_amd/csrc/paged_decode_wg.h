@@ -382,8 +382,8 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
 // merges the four states in registers with merge_states' arithmetic (max in
 // state order, then fma chains in state order), so the bits equal those of
 // decode_work_group for the same split. No LDS merge records and no
-// barriers: the waves of a work-group are independent. `tile` is the wave's
-// private K transpose tile (kTileBytes<D> bytes).
+// barriers: the wave needs no other wave. `tile` is the wave's private K
+// transpose tile (kTileBytes<D> bytes).
 template <int D, int PF>
 __device__ __forceinline__ void decode_split_wave(const DecodeArgs& a, const int item, unsigned char* tile) {
   constexpr int KC = D / 32;
