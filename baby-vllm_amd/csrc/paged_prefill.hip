@@ -28,8 +28,8 @@
 // NaN) never reach a product.
 //
 // Sequences with a single query token (the decode rows of a mixed step) are
-// instead computed by decode work-groups (paged_decode_wg.h) placed in front of
-// the prefill work-groups of the same launch: their waves split a row's pages,
+// instead computed by decode work-groups (paged_decode_wg.h) placed behind the
+// prefill work-groups of the same launch: their waves split a row's pages,
 // where a prefill work-group would walk them with one live wave.
 #include "bvllm_device.h"
 #include "bvllm_abi_internal.h"
@@ -110,11 +110,17 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   static_assert(NW == kDecodeWaves, "decode work-groups run with the prefill work-group size");
   static_assert(decode_lds_bytes<D, kDecodeWaves>(16) <= sizeof(lds), "decode work-group LDS");
 
-  // The first n_dec_wgs work-groups (a multiple of 8) are decode work-groups,
-  // one per (sequence, KV head); those past the batch have nothing to do.
-  if ((int)blockIdx.x < n_dec_wgs) {
-    if ((int)blockIdx.x < dec.batch * dec.num_kv_heads)
-      decode_work_group<D, kDecodeWaves, kDecodeDepth>(dec, blockIdx.x, reinterpret_cast<float*>(lds));
+  // The last n_dec_wgs work-groups are decode work-groups, one per (sequence,
+  // KV head); those past the batch have nothing to do. They come after the
+  // prefill work-groups so that the prefill ones, dispatched first, get their
+  // first tiles' loads in ahead of the decode work-groups' page stream, which
+  // otherwise fills each CU's memory queue in front of them (mixed step
+  // 1 x 512 + 63 decodes: 34.6 -> 29.5 us).
+  const int n_pre_wgs = (int)gridDim.x - n_dec_wgs;
+  if ((int)blockIdx.x >= n_pre_wgs) {
+    const int dw = (int)blockIdx.x - n_pre_wgs;
+    if (dw < dec.batch * dec.num_kv_heads)
+      decode_work_group<D, kDecodeWaves, kDecodeDepth>(dec, dw, reinterpret_cast<float*>(lds));
     return;
   }
 
@@ -129,7 +135,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   // by XCDs h·xcd_group .. +xcd_group-1, which deal its query blocks out in
   // boustrophedon order (0 1 | 1 0 | 0 1 ...): each L2 holds one KV head's
   // keys, and the heavy-to-light run of a sequence's blocks spreads evenly.
-  const int id = blockIdx.x - n_dec_wgs;
+  const int id = blockIdx.x;
   // The arguments that address the metadata and table loads below, read
   // with the mapping's own: otherwise their wait splits those loads' round trip.
   asm volatile("" ::"s"(a.block_tables), "s"(a.bt_stride), "s"(a.max_blocks), "s"(a.query_start_loc),
