@@ -219,3 +219,18 @@ def test_blocks_per_work_group_do_not_change_bits(bpw, hkv, group, d, monkeypatc
     many = _kernel()(q, kv_cache, md, d ** -0.5)
     assert torch.equal(one, many)
     assert_attn_close(many, _oracle(q, kv_cache, md, group))
+
+
+def test_scores_rising_with_blocks_per_work_group(monkeypatch):
+    """The rescale path on the multi-block kernel: every sequence within two
+    64-key tiles, a grid large enough for several blocks per work-group, key
+    norms growing with position; same bits as one block per work-group."""
+    specs = [(0, 128)] * 40 + [(60, 60)] * 10 + [(5, 1)]
+    q, kv_cache, md = build_prefill_case(specs, 4, 7, 128, seed=17)
+    assert md.block_tables.shape[1] <= 8
+    scale_keys_by_position(kv_cache, md.block_tables, md.seq_lens_cpu, lambda p: 1.0 + p / 12.0)
+    many = _kernel()(q, kv_cache, md, 128 ** -0.5)
+    monkeypatch.setenv("BVLLM_PREFILL_BLOCKS_PER_WG", "1")
+    one = _kernel()(q, kv_cache, md, 128 ** -0.5)
+    assert torch.equal(one, many)
+    assert_attn_close(many, _oracle(q, kv_cache, md, 7))
