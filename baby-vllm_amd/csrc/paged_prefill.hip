@@ -132,7 +132,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   // takes a contiguous range of (sequence, KV head, block), so the blocks that
   // share a prefix share an L2 and every XCD gets many whole pairs.
   // xcd_group = 8 / Hkv > 0 (few pairs, or a mixed step): KV head h is served
-  // by XCDs h·xcd_group .. +xcd_group-1, which deal its query blocks out in
+  // by XCDs h·xcd_group .. +xcd_group-1, which deal its column blocks out in
   // boustrophedon order (0 1 | 1 0 | 0 1 ...): each L2 holds one KV head's
   // keys, and the heavy-to-light run of a sequence's blocks spreads evenly.
   const int id = blockIdx.x;
