@@ -591,17 +591,23 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
 #pragma unroll
   for (int ct = 0; ct < QT; ++ct) {
     const float lt = lsum[ct][0];
-    if (!valid[ct]) continue;
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    // acc[ct][c][i] is dim 16c + 4g + i.
+    // acc[ct][c][i] is dim 16c + 4g + i. Lanes of 16-lane rows g and g^1 hold
+    // the column's two 4-dim halves of each 8-dim group: one row swap per pair
+    // of dim blocks (c, c+1) gives every lane 8 consecutive dims, stored as
+    // 16 bytes: rows g even take block c at dims 16c + 4g, rows g odd block c+1
+    // at dims 16(c+1) + 4(g-1).
     uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + (int64_t)(q_start + qi[ct]) * a.o_st +
-                     (int64_t)(kvh * G + hl[ct]) * a.o_sh + 4 * g;
+                     (int64_t)(kvh * G + hl[ct]) * a.o_sh + 4 * g + 12 * (g & 1);
 #pragma unroll
-    for (int c = 0; c < VD; ++c) {
-      uint2 pk;
-      pk.x = pack_bf16x2_hw(acc[ct][c][0] * inv, acc[ct][c][1] * inv);
-      pk.y = pack_bf16x2_hw(acc[ct][c][2] * inv, acc[ct][c][3] * inv);
-      st8(orow + 16 * c, pk);
+    for (int c = 0; c < VD; c += 2) {
+      const uint32_t x0 = pack_bf16x2_hw(acc[ct][c][0] * inv, acc[ct][c][1] * inv);
+      const uint32_t y0 = pack_bf16x2_hw(acc[ct][c][2] * inv, acc[ct][c][3] * inv);
+      const uint32_t x1 = pack_bf16x2_hw(acc[ct][c + 1][0] * inv, acc[ct][c + 1][1] * inv);
+      const uint32_t y1 = pack_bf16x2_hw(acc[ct][c + 1][2] * inv, acc[ct][c + 1][3] * inv);
+      const auto sx = __builtin_amdgcn_permlane16_swap(x0, x1, false, false);
+      const auto sy = __builtin_amdgcn_permlane16_swap(y0, y1, false, false);
+      if (valid[ct]) st16(orow + 16 * c, make_uint4(sx[0], sy[0], sx[1], sy[1]));
     }
   }
   if (!MB) break;
