@@ -203,14 +203,15 @@ def test_scores_rising_along_the_sequence(growth, hkv, group, d):
 
 
 @pytest.mark.parametrize("bpw", [2, 3, 4, 7, 64])
-@pytest.mark.parametrize("hkv,group,d", [(4, 7, 128), (8, 3, 64)])
+@pytest.mark.parametrize("hkv,group,d", [(4, 7, 128), (8, 3, 64), (1, 16, 128)])
 def test_blocks_per_work_group_do_not_change_bits(bpw, hkv, group, d, monkeypatch):
     """When every sequence fits two 64-key tiles (table width ≤ 8 pages), a
     work-group may compute several column blocks of one (sequence, KV head)
     over tiles staged once; any number of blocks per work-group gives the
     bits of one block per work-group. (Both head configurations give a grid
     of at least two work-groups per CU, where the override applies.)"""
-    specs = [(0, 128)] * 20 + [(0, 77), (37, 90), (100, 28), (0, 1), (5, 3), (64, 64), (127, 1)]
+    specs = [(0, 128)] * (20 if hkv > 1 else 40) + [(0, 77), (37, 90), (100, 28), (0, 1), (5, 3), (64, 64),
+                                                    (127, 1)]
     q, kv_cache, md = build_prefill_case(specs, hkv, group, d, seed=bpw)
     assert md.block_tables.shape[1] <= 8
     monkeypatch.setenv("BVLLM_PREFILL_BLOCKS_PER_WG", "1")
