@@ -94,31 +94,44 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_chunks_kernel(const T* 
       const int c = lo + (threadIdx.x + k * kArgmaxThreads) * VEC;
       raw[k] = c < hi ? ld16(x + c) : make_uint4(0, 0, 0, 0);
     }
-    float m = -__builtin_huge_valf();
-    bool any_nan = false;
+    // Max and NaN flag as trees over the thread's PER·VEC elements (short
+    // dependence chains), then the first column holding the max (or the first
+    // NaN) as a tree of minima over candidate columns.
+    constexpr int NE = PER * VEC;
+    float vals[NE];
+    int cols[NE];
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
       const int c = lo + (threadIdx.x + k * kArgmaxThreads) * VEC;
       const T* e = reinterpret_cast<const T*>(&raw[k]);
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
-        const float v = c + j < hi ? to_f32<T>(e[j]) : -__builtin_huge_valf();
-        m = fmaxf(m, v);
-        any_nan |= v != v;
+        cols[k * VEC + j] = c + j;
+        vals[k * VEC + j] = c + j < hi ? to_f32<T>(e[j]) : -__builtin_huge_valf();
       }
     }
-    int first = 0x7fffffff;
+    float mx[NE];
+    bool nn[NE];
 #pragma unroll
-    for (int k = PER - 1; k >= 0; --k) {
-      const int c = lo + (threadIdx.x + k * kArgmaxThreads) * VEC;
-      const T* e = reinterpret_cast<const T*>(&raw[k]);
+    for (int i = 0; i < NE; ++i) { mx[i] = vals[i]; nn[i] = vals[i] != vals[i]; }
 #pragma unroll
-      for (int j = VEC - 1; j >= 0; --j) {
-        const float v = to_f32<T>(e[j]);
-        const bool hit = c + j < hi && (any_nan ? v != v : v == m);
-        first = hit ? c + j : first;
-      }
+    for (int s = 1; s < NE; s *= 2)
+#pragma unroll
+      for (int i = 0; i + s < NE; i += 2 * s) { mx[i] = fmaxf(mx[i], mx[i + s]); nn[i] = nn[i] || nn[i + s]; }
+    const float m = mx[0];
+    const bool any_nan = nn[0];
+    int fi[NE];
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const float v = vals[i];
+      const bool hit = cols[i] < hi && (any_nan ? v != v : v == m);
+      fi[i] = hit ? cols[i] : 0x7fffffff;
     }
+#pragma unroll
+    for (int s = 1; s < NE; s *= 2)
+#pragma unroll
+      for (int i = 0; i + s < NE; i += 2 * s) fi[i] = min(fi[i], fi[i + s]);
+    const int first = fi[0];
     if (first != 0x7fffffff) {
       b.v = any_nan ? __builtin_nanf("") : m;
       b.i = first;
