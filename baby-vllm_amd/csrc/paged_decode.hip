@@ -266,12 +266,18 @@ static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
   const int G = a.num_heads / a.num_kv_heads;
   const size_t smem = decode_lds_bytes<D, NW>(G);
   if (smem > 160 * 1024) return hipErrorInvalidValue;
-  static bool attr_set = false;
-  if (!attr_set) {
+  // The dynamic-LDS limit is a per-device function attribute: set once per
+  // device (setting it twice, from racing host threads, is harmless).
+  static bool attr_set[64] = {};
+  int dev = 0;
+  hipError_t de = hipGetDevice(&dev);
+  if (de != hipSuccess) return de;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  if (!attr_set[dev]) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_decode_kernel<D, NW, PF>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
-    attr_set = true;
+    attr_set[dev] = true;
   }
   const int64_t groups = (a.num_splits + a.splits_per_wg - 1) / a.splits_per_wg;
   const int64_t wgs = (int64_t)a.batch * a.num_kv_heads * groups;
