@@ -11,6 +11,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 
 namespace bvllm {
 
@@ -200,17 +201,18 @@ static hipError_t launch_reduce(const DecodeArgs& r, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Compute units of the current device (cached per device).
+// Compute units of the current device (cached per device; host threads that
+// race on the first query store the same value).
 int device_cus() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int v = 0;
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-    cached[dev] = v;
+    cached[dev].store(v, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return v;
 }
 
 // Consecutive splits per work-group: about two work-groups per compute unit
@@ -268,16 +270,16 @@ static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
   if (smem > 160 * 1024) return hipErrorInvalidValue;
   // The dynamic-LDS limit is a per-device function attribute: set once per
   // device (setting it twice, from racing host threads, is harmless).
-  static bool attr_set[64] = {};
+  static std::atomic<bool> attr_set[64] = {};
   int dev = 0;
   hipError_t de = hipGetDevice(&dev);
   if (de != hipSuccess) return de;
   if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-  if (!attr_set[dev]) {
+  if (!attr_set[dev].load(std::memory_order_acquire)) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_decode_kernel<D, NW, PF>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
-    attr_set[dev] = true;
+    attr_set[dev].store(true, std::memory_order_release);
   }
   const int64_t groups = (a.num_splits + a.splits_per_wg - 1) / a.splits_per_wg;
   const int64_t wgs = (int64_t)a.batch * a.num_kv_heads * groups;
