@@ -270,3 +270,33 @@ def test_scores_rising_along_the_row(partition):
     scale_keys_by_position(kv_cache, bt, lens, lambda p: 1.0 + p / 64.0)
     actual = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=3000, partition_blocks=partition)
     assert_attn_close(actual, _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
+
+
+# ------------------------------------------------------- seeded random batches
+
+_HEAD_CONFIGS = [(4, 7, 128), (2, 7, 64), (1, 16, 128), (8, 4, 128), (4, 1, 64), (2, 3, 64)]
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_ragged_batches(seed):
+    """Seeded random batches: 1-40 rows of 0-3000 tokens (a tenth of them
+    padded, length 0), a bucket at or above the longest row, random head
+    configurations and partition sizes (auto, single pass, 1-16 pages)."""
+    g = torch.Generator().manual_seed(3000 + seed)
+    hkv, group, d = _HEAD_CONFIGS[int(torch.randint(len(_HEAD_CONFIGS), (1,), generator=g))]
+    B = int(torch.randint(1, 41, (1,), generator=g))
+    lens = [0 if int(torch.randint(10, (1,), generator=g)) == 0 else int(torch.randint(1, 3001, (1,), generator=g))
+            for _ in range(B)]
+    if max(lens) == 0:
+        lens[0] = 1
+    bucket = max(lens) + int(torch.randint(0, 65, (1,), generator=g))
+    choice = int(torch.randint(18, (1,), generator=g))
+    partition = None if choice == 17 else choice  # 0 = single pass
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, hkv=hkv, group=group, d=d,
+                                                   width=cdiv(bucket, BLOCK_SIZE) + 1, seed=seed)
+    scale = d ** -0.5
+    actual = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=bucket, partition_blocks=partition)
+    assert_attn_close(actual, _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
+    for row in range(B):
+        if lens[row] == 0:
+            assert actual[row].abs().max() == 0

@@ -235,3 +235,51 @@ def test_scores_rising_with_blocks_per_work_group(monkeypatch):
     one = _kernel()(q, kv_cache, md, 128 ** -0.5)
     assert torch.equal(one, many)
     assert_attn_close(many, _oracle(q, kv_cache, md, 7))
+
+
+# ------------------------------------------------------- seeded random batches
+
+_HEAD_CONFIGS = [(4, 7, 128), (2, 7, 64), (1, 16, 128), (8, 4, 128), (4, 1, 64), (2, 3, 64)]
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_varlen_batches(seed):
+    """Seeded random steps: 1-12 sequences, each with a cached prefix of 0-700
+    tokens and 0-300 new queries (a quarter of them single-query rows), over
+    random head configurations."""
+    g = torch.Generator().manual_seed(1000 + seed)
+    hkv, group, d = _HEAD_CONFIGS[int(torch.randint(len(_HEAD_CONFIGS), (1,), generator=g))]
+    specs = []
+    for _ in range(int(torch.randint(1, 13, (1,), generator=g))):
+        ctx = int(torch.randint(0, 701, (1,), generator=g))
+        kind = int(torch.randint(4, (1,), generator=g))
+        q_len = 1 if kind == 0 else int(torch.randint(0, 301, (1,), generator=g))
+        specs.append((ctx, q_len))
+    if max(n for _, n in specs) == 0:
+        specs[0] = (specs[0][0], 1)
+    q, kv_cache, md = build_prefill_case(specs, hkv, group, d, seed=seed)
+    actual = _kernel()(q, kv_cache, md, d ** -0.5)
+    assert_attn_close(actual, _oracle(q, kv_cache, md, group))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_short_batches_against_one_block_per_work_group(seed, monkeypatch):
+    """Seeded random steps of 24-80 sequences that all fit two 64-key tiles,
+    where the host gives a work-group several column blocks whenever the grid
+    allows it: within tolerance of the oracle and bit-equal to one block per
+    work-group."""
+    g = torch.Generator().manual_seed(2000 + seed)
+    hkv, group, d = _HEAD_CONFIGS[seed % len(_HEAD_CONFIGS)]
+    specs = []
+    for _ in range(int(torch.randint(24, 81, (1,), generator=g))):
+        q_len = int(torch.randint(1, 129, (1,), generator=g))
+        ctx = int(torch.randint(0, 129 - q_len, (1,), generator=g))
+        specs.append((ctx, q_len))
+    q, kv_cache, md = build_prefill_case(specs, hkv, group, d, seed=seed)
+    assert md.block_tables.shape[1] <= 8
+    monkeypatch.delenv("BVLLM_PREFILL_BLOCKS_PER_WG", raising=False)
+    auto = _kernel()(q, kv_cache, md, d ** -0.5)
+    monkeypatch.setenv("BVLLM_PREFILL_BLOCKS_PER_WG", "1")
+    one = _kernel()(q, kv_cache, md, d ** -0.5)
+    assert torch.equal(auto, one)
+    assert_attn_close(auto, _oracle(q, kv_cache, md, group))
