@@ -176,3 +176,38 @@ def test_rejects_wrong_dtypes_and_cpu_tensors():
         _kernel()(q, k, k, cos, cos)
     with pytest.raises(RuntimeError):
         _kernel()(q.cpu().bfloat16(), k.cpu(), k.cpu(), cos.cpu(), cos.cpu())
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_steps_bitwise(seed):
+    """Seeded random steps: 1-600 tokens, random head shapes, q/k/v as views of
+    one fused QKV row or as separate tensors, scattered slots, with or without
+    the cache; every output bit-equal to the oracle."""
+    g = torch.Generator().manual_seed(4000 + seed)
+    H, Hkv, D = [(28, 4, 128), (14, 2, 64), (8, 8, 128), (12, 2, 64), (32, 8, 128)][seed % 5]
+    T = int(torch.randint(1, 601, (1,), generator=g))
+    fused = bool(torch.randint(2, (1,), generator=g))
+    with_cache = seed % 4 != 3
+    gd = torch.Generator(device="cuda").manual_seed(seed)
+    if fused:
+        _, q, k, v = _qkv(T, H, Hkv, D, seed)
+    else:
+        q = torch.randn(T, H, D, device="cuda", dtype=torch.bfloat16, generator=gd)
+        k = torch.randn(T, Hkv, D, device="cuda", dtype=torch.bfloat16, generator=gd)
+        v = torch.randn(T, Hkv, D, device="cuda", dtype=torch.bfloat16, generator=gd)
+    pos = torch.randint(0, 8192, (T,), generator=g).to("cuda")
+    inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, dtype=torch.float32, device="cuda") / D))
+    ang = pos[:, None].float() * inv[None]
+    cos = torch.cat([ang.cos(), ang.cos()], -1).to(torch.bfloat16)
+    sin = torch.cat([ang.sin(), ang.sin()], -1).to(torch.bfloat16)
+    cache = slots = None
+    if with_cache:
+        nb = (T + BLOCK_SIZE - 1) // BLOCK_SIZE + 3
+        cache = torch.randn(2, nb, BLOCK_SIZE, Hkv, D, device="cuda", dtype=torch.bfloat16, generator=gd)
+        slots = torch.randperm(nb * BLOCK_SIZE, generator=g)[:T].to(torch.int64).to("cuda")
+    qr, kr, cr = _oracle(q, k, v, cos, sin, cache, slots)
+    _kernel()(q, k, v, cos, sin, cache, slots)
+    torch.cuda.synchronize()
+    assert _bits_equal(q, qr) and _bits_equal(k, kr)
+    if with_cache:
+        assert _bits_equal(cache, cr)
