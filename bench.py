@@ -415,8 +415,8 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the paged-KV kernels shard by KV head or sequence with no exchange; "
-              "see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(the paged-KV kernels would shard by KV head or by sequence, with no "
+              "exchange inside attention). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
