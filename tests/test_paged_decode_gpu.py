@@ -300,3 +300,29 @@ def test_random_ragged_batches(seed):
     for row in range(B):
         if lens[row] == 0:
             assert actual[row].abs().max() == 0
+
+
+# ------------------------------------------- reduce over more than one set of groups
+
+def test_more_splits_than_one_reduce_set():
+    """Partition 1 over rows of 20000 and 17001 tokens: 1250 splits, more
+    than the 32 x 32 that one reduce pass holds, so the reduce takes the max
+    in a pass of its own and adds the sets' group sums in order."""
+    lens = [20000, 17001, 0]
+    scale = HEAD_DIM ** -0.5
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, seed=21)
+    assert cdiv(max(lens), BLOCK_SIZE) > 32 * 32
+    actual = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=max(lens), partition_blocks=1)
+    assert_attn_close(actual, _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
+    assert actual[2].abs().max() == 0
+
+
+def test_reduce_sets_do_not_change_bits():
+    """A 600-token row with partition 1: 38 splits eagerly, 1100 under a wide
+    graph bucket (several reduce sets, trailing splits empty); same bits."""
+    scale = HEAD_DIM ** -0.5
+    q, kv_cache, bt, seq_lens = make_decode_inputs([600], width=1102, seed=22)
+    eager = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=600, partition_blocks=1)
+    graph = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=1100 * BLOCK_SIZE, partition_blocks=1)
+    assert torch.equal(eager, graph)
+    assert_attn_close(graph, _oracle(q, kv_cache, bt, [600], scale))

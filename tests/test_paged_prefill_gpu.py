@@ -283,3 +283,24 @@ def test_random_short_batches_against_one_block_per_work_group(seed, monkeypatch
     one = _kernel()(q, kv_cache, md, d ** -0.5)
     assert torch.equal(auto, one)
     assert_attn_close(auto, _oracle(q, kv_cache, md, group))
+
+
+# ------------------------------------------------- beyond the oracle's sizes
+
+@pytest.mark.parametrize("hkv,group,d", [(4, 7, 128), (2, 7, 64)])
+def test_long_sequence_with_one_key_repeated(hkv, group, d):
+    """1 x (8192 cached + 8192 new) tokens, every key the same vector: each
+    query's scores are equal, so its output is the mean of the values it sees
+    (keys 0 .. ctx + i), a closed form checked at a size where the CPU oracle
+    would take minutes. The scores are not zero, so the QKᵀ path and the max
+    reference still run."""
+    ctx, n = 8192, 8192
+    q, kv_cache, md = build_prefill_case([(ctx, n)], hkv, group, d, seed=5, nan_fill=False)
+    key = torch.randn(hkv, d, device="cuda", dtype=torch.bfloat16)
+    kv_cache[0] = key
+    pages = md.block_tables[0].long()
+    v = kv_cache[1, pages].reshape(-1, hkv, d)[: ctx + n].double()  # [keys, Hkv, D] in order
+    prefix_mean = v.cumsum(0) / torch.arange(1, ctx + n + 1, device="cuda", dtype=torch.float64)[:, None, None]
+    expected = prefix_mean[ctx:].repeat_interleave(group, dim=1)  # [n, H, D]
+    actual = _kernel()(q, kv_cache, md, d ** -0.5)
+    assert_attn_close(actual, expected)
