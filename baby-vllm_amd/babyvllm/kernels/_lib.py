@@ -48,6 +48,17 @@ SIGNATURES = {
         _i32, _i32, _i32, _i32, _i32, _i32,  # B, H, Hkv, D, block_size, waves
         _p,                         # stream
     ]),
+    "bvllm_paged_decode_noalloc": (ctypes.c_int, [
+        _p, _i64, _i64,             # q
+        _p, _p, _i64, _i64, _i64,   # caches + strides
+        _i32,                       # num_blocks
+        _p, _i64, _i32,             # block_tables, bt_stride, max_blocks
+        _p, _f32,                   # seq_lens, scale
+        _p, _i64, _i64,             # out
+        _i32, _i32,                 # num_splits, blocks_per_split
+        _i32, _i32, _i32, _i32, _i32, _i32,  # B, H, Hkv, D, block_size, waves
+        _p,                         # stream
+    ]),
     "bvllm_paged_prefill": (ctypes.c_int, [
         _p, _i64, _i64,             # q
         _p, _p, _i64, _i64, _i64,   # caches + strides
@@ -76,7 +87,7 @@ SIGNATURES = {
     "bvllm_silu_mul": (ctypes.c_int, [_p, _i64, _i32, _p, _p]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class KernelLibraryError(RuntimeError):

@@ -23,6 +23,8 @@ extern "C" int bvllm_abi_version(void) { return BVLLM_ABI_VERSION; }
 
 extern "C" const char* bvllm_error_string(int code) {
   if (code == kBad) return "invalid argument (rejected by babyvllm_amd)";
+  if (code == BVLLM_ERROR_SCRATCH_LIMIT)
+    return "decode split scratch exceeds BVLLM_NOALLOC_SCRATCH_BYTES (use bvllm_paged_decode with a workspace)";
   return hipGetErrorString((hipError_t)code);
 }
 

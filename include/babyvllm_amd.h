@@ -37,7 +37,7 @@ extern "C" {
 #endif
 
 /* ABI version of this header; bumped on any signature change. */
-#define BVLLM_ABI_VERSION 4
+#define BVLLM_ABI_VERSION 5
 
 #if defined(__GNUC__)
 #define BVLLM_API __attribute__((visibility("default")))
@@ -107,6 +107,36 @@ BVLLM_API int bvllm_paged_decode(const void* q, int64_t q_stride_b, int64_t q_st
                        void* workspace, int32_t num_splits, int32_t blocks_per_split,
                        int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                        int32_t head_dim, int32_t block_size, int32_t waves, void* stream);
+
+/*
+ * bvllm_paged_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under hipGraph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference: its
+ * decode allocates the split scratch through torch on every call
+ * (babyvllm/kernels/paged_attn.py:317-320).
+ *
+ * Same arguments, kernels and results as bvllm_paged_decode; the split
+ * partials go to a static device array of BVLLM_NOALLOC_SCRATCH_BYTES per GPU,
+ * owned by the library until the process ends. The call allocates and frees
+ * nothing. A launch whose bvllm_decode_workspace_bytes() exceeds that size is
+ * rejected with BVLLM_ERROR_SCRATCH_LIMIT before anything is launched.
+ * Every call on one GPU shares that GPU's array: calls that overlap in time on
+ * one GPU (different streams, or different host threads) race and must not be
+ * issued; calls ordered on one stream are fine. Nothing in the array needs to
+ * start at zero: every launch writes each partial it later reads.
+ */
+#define BVLLM_NOALLOC_SCRATCH_BYTES (32ll << 20)
+#define BVLLM_ERROR_SCRATCH_LIMIT 10001
+BVLLM_API int bvllm_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                         const void* k_cache, const void* v_cache,
+                                         int64_t cache_stride_block, int64_t cache_stride_tok,
+                                         int64_t cache_stride_head, int32_t num_blocks,
+                                         const int32_t* block_tables, int64_t bt_stride, int32_t max_blocks,
+                                         const int32_t* seq_lens, float scale,
+                                         void* out, int64_t out_stride_b, int64_t out_stride_h,
+                                         int32_t num_splits, int32_t blocks_per_split,
+                                         int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, int32_t block_size, int32_t waves, void* stream);
 
 /*
  * Varlen paged prefill attention. Replaces paged_prefill_attention
