@@ -56,6 +56,10 @@ class KVCacheManager:
         return len(self.free_block_ids)
 
     @property
+    def num_used_blocks(self) -> int:
+        return self.num_blocks - len(self.free_block_ids)
+
+    @property
     def prefix_cache_hit_rate(self) -> float:
         return self.num_hit_tokens / self.num_queried_tokens if self.num_queried_tokens else 0.0
 

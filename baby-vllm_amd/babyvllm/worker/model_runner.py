@@ -82,6 +82,11 @@ class ModelRunner:
         self._graphs: dict[tuple[int, int], torch.cuda.CUDAGraph] = {}
         self._pool = None
         self._decode_inputs: DecodeInputs | None = None
+        # Observability for tests and benchmarks: decode steps served by a graph
+        # replay, and an optional callable(seqs, logits) shown every step's
+        # logits rows (row i belongs to seqs[i]) before sampling.
+        self.graph_replays = 0
+        self.logits_observer = None
         self.max_blocks_per_seq = -(-max(CTX_BUCKETS) // self.block_size) + 1
 
     # ------------------------------------------------------------- KV cache
@@ -167,6 +172,8 @@ class ModelRunner:
             hidden = self.model(input_ids, positions)
         last = torch.tensor([e - 1 for e in md.query_start_loc_cpu[1:]], device=self.device)
         logits = self.model.compute_logits(hidden[last])
+        if self.logits_observer is not None:
+            self.logits_observer(scheduler_output.scheduled_sequences, logits)
         return self._sample(logits, scheduler_output.scheduled_sequences)
 
     # ---------------------------------------------------------- graph steps
@@ -259,6 +266,9 @@ class ModelRunner:
         buf = self.prepare_decode_inputs(seqs, scheduler_output.block_tables, bb, cb)
         graph = self.capture_one(bb, cb)
         graph.replay()
+        self.graph_replays += 1
+        if self.logits_observer is not None:
+            self.logits_observer(seqs, buf.logits[:n])
         if all(s.sampling_params.temperature == 0.0 for s in seqs):
             host = self._decode_inputs
             host.t_tokens[:bb].copy_(buf.tokens, non_blocking=True)
