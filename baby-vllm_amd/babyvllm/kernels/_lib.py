@@ -71,6 +71,7 @@ SIGNATURES = {
         _i32, _i32, _i32, _i32,     # H, Hkv, D, block_size
         _p,                         # stream
     ]),
+    "bvllm_set_tuning": (ctypes.c_int, [_i32, _i32]),
     "bvllm_argmax_workspace_bytes": (ctypes.c_int64, [_i32, _i32]),
     "bvllm_greedy_argmax": (ctypes.c_int, [
         _p, _i64, _i32, _i32,       # logits, row_stride, rows, vocab
@@ -87,7 +88,15 @@ SIGNATURES = {
     "bvllm_silu_mul": (ctypes.c_int, [_p, _i64, _i32, _p, _p]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
+
+
+# Knobs of bvllm_set_tuning (include/babyvllm_amd.h).
+TUNE_DECODE_SPLIT_MODE = 0
+TUNE_PREFILL_BLOCKS_PER_WG = 1
+TUNE_DECODE_ORDER = 2
+TUNE_DECODE_SINGLE_PASS_STREAM = 3
+TUNE_DECODE_CACHED = 4
 
 
 class KernelLibraryError(RuntimeError):
@@ -109,6 +118,14 @@ def lib() -> ctypes.CDLL:
     if got != ABI_VERSION:
         raise KernelLibraryError(f"{LIB_PATH} has ABI {got}, expected {ABI_VERSION}: rebuild it")
     return handle
+
+
+def set_tuning(knob: int, value: int) -> int:
+    """Sets a process-wide tuning knob (0 = default); returns its previous value."""
+    prev = lib().bvllm_set_tuning(knob, value)
+    if prev < 0:
+        raise ValueError(f"unknown tuning knob {knob}")
+    return prev
 
 
 def check(rc: int, what: str) -> None:

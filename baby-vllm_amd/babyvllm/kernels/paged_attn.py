@@ -16,26 +16,16 @@ no device-to-host read.
 from __future__ import annotations
 
 import functools
-import os
 
 import torch
 
 from babyvllm.kernels import _lib
 from babyvllm.kernels.decode_split import decode_split_plan
 
-# Waves per decode work-group: "auto" (the library's choice) or 8.
-DECODE_WAVES_ENV = "BVLLM_DECODE_WAVES"
-
 
 @functools.lru_cache(maxsize=None)
 def _num_sms(device_index: int) -> int:
     return torch.cuda.get_device_properties(device_index).multi_processor_count
-
-
-def decode_waves() -> int:
-    """Waves per work-group to request: 0 lets the library choose."""
-    setting = os.environ.get(DECODE_WAVES_ENV, "auto")
-    return 0 if setting == "auto" else int(setting)
 
 
 def _device_index(t: torch.Tensor) -> int:
@@ -93,7 +83,7 @@ def paged_decode_attention(q, kv_cache, block_tables, seq_lens, scale,
         seq_lens.data_ptr(), float(scale),
         out.data_ptr(), out.stride(0), out.stride(1),
         None if workspace is None else workspace.data_ptr(), num_splits, blocks_per_split,
-        B, n_heads, n_kv_heads, head_dim, block_size, decode_waves(),
+        B, n_heads, n_kv_heads, head_dim, block_size, 0,
         _lib.stream_handle(q.device),
     )
     _lib.check(rc, "bvllm_paged_decode")

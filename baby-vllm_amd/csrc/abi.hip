@@ -73,12 +73,8 @@ extern "C" int64_t bvllm_decode_workspace_bytes(int32_t batch, int32_t num_heads
                                                 int32_t head_dim, int32_t num_splits,
                                                 int32_t blocks_per_split) {
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_splits < 1 || blocks_per_split < 1) return 0;
-  DecodeArgs a{};
-  a.batch = batch;
-  a.num_splits = num_splits;
-  a.blocks_per_split = blocks_per_split;
-  const int64_t parts = decode_partials(a);
-  if (parts <= 1) return 0;
+  const int64_t parts = decode_partials(batch, num_kv_heads, num_splits, blocks_per_split);
+  if (parts <= 0) return 0;
   const int64_t rows = (int64_t)batch * num_heads * parts;
   return rows * head_dim * (int64_t)sizeof(float) + rows * (int64_t)sizeof(float);
 }
@@ -116,7 +112,7 @@ extern "C" int bvllm_paged_decode(const void* q, int64_t q_stride_b, int64_t q_s
   const int64_t ws_bytes = bvllm_decode_workspace_bytes(batch, num_heads, num_kv_heads, head_dim, num_splits,
                                                         blocks_per_split);
   if (ws_bytes > 0 && (!workspace || !aligned16(workspace))) return kBad;
-  if (waves != 0 && waves != 4 && waves != 8) return kBad;
+  if (waves != 0 && waves != 4) return kBad;
 
   DecodeArgs a{};
   a.q = q; a.q_sb = q_stride_b; a.q_sh = q_stride_h;
@@ -180,6 +176,8 @@ extern "C" int bvllm_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_
   a.single_query_seqs = single_query_seqs;
   return (int)paged_prefill(a, (hipStream_t)stream);
 }
+
+extern "C" int bvllm_set_tuning(int32_t knob, int32_t value) { return set_tuning(knob, value); }
 
 extern "C" int64_t bvllm_argmax_workspace_bytes(int32_t rows, int32_t vocab) {
   if (rows <= 0 || vocab <= 0) return 0;

@@ -35,8 +35,11 @@ struct DecodeArgs {
   float* part_lse;                         // [B, H, parts] fp32 (log2 units)
   int32_t num_splits, blocks_per_split;
   int32_t batch, num_heads, num_kv_heads, head_dim;
-  int32_t waves;                           // waves per work-group (4 or 8; 0 = default)
-  int32_t splits_per_wg;                   // consecutive splits one work-group computes (set by the launcher)
+  int32_t waves;                           // waves per single-pass work-group (4; 0 = default)
+  // Set by the launcher for split launches (decode_plan):
+  int32_t splits_per_item;                 // consecutive splits one streaming wave computes
+  int32_t num_partials;                    // partial states per (row, head) in the workspace
+  int32_t item_order;                      // 0: KV head fastest in the wave numbering; 1: split unit fastest
   // Prefill view (both null for a decode batch): row b is sequence b of a
   // varlen prefill batch. Only sequences with exactly one query token are
   // computed; their q / out row is query_start_loc[b] and they attend keys
@@ -97,8 +100,30 @@ hipError_t greedy_argmax(const ArgmaxArgs& a, hipStream_t stream);
 hipError_t fused_add_rms_norm(const NormArgs& a, hipStream_t stream);
 hipError_t silu_mul(const SiluArgs& a, hipStream_t stream);
 hipError_t paged_decode(const DecodeArgs& a, hipStream_t stream);
+
+// How a decode launch with the caller's split plan runs (paged_decode.hip).
+struct DecodePlan {
+  bool single_pass;        // one split: single-pass work-groups, no workspace
+  int32_t group;           // consecutive splits folded into one partial (level 2 of the merge)
+  int32_t splits_per_item; // splits per streaming wave: 1, or `group` when the wave folds them
+  int32_t partials;        // partial states per (row, head) in the workspace
+  bool fold_in_reduce;     // the reduce folds the per-split partials into groups
+};
+DecodePlan decode_plan(int32_t batch, int32_t num_kv_heads, int32_t num_splits, int32_t blocks_per_split);
 // Partial states (per row and head) one decode launch writes to the workspace.
-int32_t decode_partials(const DecodeArgs& a);
+int32_t decode_partials(int32_t batch, int32_t num_kv_heads, int32_t num_splits, int32_t blocks_per_split);
+
+// Process-wide tuning switches (bvllm_set_tuning). Knob values: 0 = default.
+enum TuneKnob {
+  kTuneDecodeSplitMode = 0,         // 1: one wave per split, 2: one wave per group of splits (same bits)
+  kTunePrefillBlocksPerWg = 1,      // n > 0: prefill column blocks per work-group when the table allows it
+  kTuneDecodeOrder = 2,             // 1: split units fastest in the streaming wave numbering (same bits)
+  kTuneDecodeSinglePassStream = 3,  // 1: single-pass launches on streaming waves too (same bits)
+  kTuneDecodeCached = 4,            // 1: streaming page loads without the nontemporal hint (same bits)
+  kTuneKnobs = 5,
+};
+int tuning(int knob);
+int set_tuning(int knob, int value);
 hipError_t paged_prefill(const PrefillArgs& a, hipStream_t stream);
 // Compute units of the current device (cached per device).
 int device_cus();

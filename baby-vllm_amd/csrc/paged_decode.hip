@@ -3,12 +3,11 @@
 //
 // Replaces paged_decode_attn_kernel, paged_decode_attn_split_kernel and
 // paged_decode_attn_reduce_kernel (babyvllm/kernels/paged_attn.py:9-251).
-// The work-group body (page walk, MFMA products, in-LDS merge of the waves) is
-// decode_work_group in paged_decode_wg.h; this file holds the kernels that
-// launch it, the split reduce, and the launch choices.
-#include "paged_decode_wg.h"
-
-#include <stdlib.h>
+// The single-pass work-group is decode_work_group (paged_decode_wg.h), the
+// split waves are decode_stream_wave (paged_decode_stream.h); this file holds
+// the kernels that launch them, the split reduce, the launch plan and the
+// tuning switches.
+#include "paged_decode_stream.h"
 
 #include <algorithm>
 #include <atomic>
@@ -21,58 +20,56 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
   decode_work_group<D, NW, PF>(a, blockIdx.x, smem);
 }
 
-// Many short splits: one split per wave (decode_split_wave), one wave per
-// work-group, so that a short batch's splits spread over every CU (B8 x 1920:
-// 480 splits on 480 work-groups instead of 120 four-wave ones, 15.5 -> 14.1 us;
-// two waves per work-group 14.4, four pages in flight per wave slower at any
-// work-group size).
-template <int D, int PF>
-__global__ __launch_bounds__(64) void paged_decode_split_wave_kernel(DecodeArgs a, int items) {
+// One streaming wave per work-group, so that a short batch's splits spread
+// over every CU.
+template <int D, int PF, bool NT, bool GROUP>
+__global__ __launch_bounds__(64) void paged_decode_stream_kernel(DecodeArgs a, int items) {
   __shared__ __attribute__((aligned(16))) unsigned char tile[kTileBytes<D>];
   const int item = (int)blockIdx.x;
   if (item >= items) return;
-  decode_split_wave<D, PF>(a, item, tile);
+  decode_stream_wave<D, PF, NT, GROUP>(a, item, tile);
 }
 
-// Split reduce: out = Σ_s w_s·o_s / Σ_s w_s, w_s = 2^(lse_s − max lse), over the
-// S partial states of a (row, head). Both reduce kernels use the same
-// arithmetic, so a row's bits do not depend on S beyond its empty splits
-// (w = 0, o = 0; eager and graph launches differ only in those):
-//   * splits are taken in groups of kReduceGroup consecutive splits; a group's
-//     sums are fma chains in split order: num = fma(w_s, o_s, num), den += w_s;
-//   * group sums are added in group order, skipping groups with den == 0.
-// With S ≤ kReduceGroup there is one group and its chain is the result.
-constexpr int kReduceGroup = 32;
+// ---------------------------------------------------------------- the reduce
+//
+// Level 3 of the split merge: out = Σ_g w_g·o_g / Σ_g w_g, w_g = 2^(lse_g − M),
+// M the largest lse_g, over the group results g of a (row, head), in order:
+//   * groups are taken in chains of kChain consecutive groups; a chain's sums
+//     are fma chains in group order: num = fma(w_g, o_g, num), den += w_g;
+//   * chain sums are added in chain order, skipping chains with den == 0.
+// With at most kChain groups that is one chain. When the split waves wrote one
+// partial per split and the plan groups splits (level 2 not yet done), the
+// reduce first folds each group's splits (GroupFold).
+constexpr int kChain = 32;
 
-// One group's partial states for 4 dims, loaded in one round.
-struct ReduceGroup {
-  float l[kReduceGroup];
-  float4 x[kReduceGroup];
+// One chain's partial states for 4 dims, loaded in one round.
+struct ChainRegs {
+  float l[kChain];
+  float4 x[kChain];
 };
 
-__device__ __forceinline__ void load_group(ReduceGroup& r, const float* lse, const float* po, int D, int s0,
-                                           int S) {
+__device__ __forceinline__ void load_chain(ChainRegs& r, const float* lse, const float* po, int D, int s0, int n) {
 #pragma unroll
-  for (int k = 0; k < kReduceGroup; ++k) {
+  for (int k = 0; k < kChain; ++k) {
     const int s = s0 + k;
-    r.l[k] = s < S ? lse[s] : kNegInf;
-    r.x[k] = s < S ? *reinterpret_cast<const float4*>(po + (int64_t)s * D) : make_float4(0.f, 0.f, 0.f, 0.f);
+    r.l[k] = s < n ? lse[s] : kNegInf;
+    r.x[k] = s < n ? *reinterpret_cast<const float4*>(po + (int64_t)s * D) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
 }
 
-__device__ __forceinline__ float group_max(const ReduceGroup& r) {
+__device__ __forceinline__ float chain_max(const ChainRegs& r) {
   float M = kNegInf;
 #pragma unroll
-  for (int k = 0; k < kReduceGroup; ++k) M = fmaxf(M, r.l[k]);
+  for (int k = 0; k < kChain; ++k) M = fmaxf(M, r.l[k]);
   return M;
 }
 
-// The group's fma chains in split order.
-__device__ __forceinline__ void chain_group(const ReduceGroup& r, float M, float4& num, float& den) {
+// The chain's fma sums in group order.
+__device__ __forceinline__ void chain_sums(const ChainRegs& r, float M, float4& num, float& den) {
   num = make_float4(0.f, 0.f, 0.f, 0.f);
   den = 0.f;
 #pragma unroll
-  for (int k = 0; k < kReduceGroup; ++k) {
+  for (int k = 0; k < kChain; ++k) {
     const float wgt = fast_exp2(r.l[k] - M);
     num.x = __builtin_fmaf(wgt, r.x[k].x, num.x);
     num.y = __builtin_fmaf(wgt, r.x[k].y, num.y);
@@ -93,58 +90,86 @@ __device__ __forceinline__ void store_reduced(const DecodeArgs& a, int64_t bh, i
   st8(dst, pk);
 }
 
-// S ≤ kReduceGroup: one thread per (row, head, 4 dims), one group.
-template <int D>
+// At most kChain group results per (row, head): one thread per (row, head,
+// 4 dims). FOLD: the workspace holds one partial per split (at most kChain of
+// them), folded here into groups of kSplitGroup first.
+template <int D, bool FOLD>
 __global__ __launch_bounds__(256) void decode_reduce_small_kernel(DecodeArgs a, int64_t items) {
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= items) return;
   const int64_t bh = t / (D / 4);
   const int d = (int)(t - bh * (D / 4)) * 4;
-  const int S = a.num_splits;
-  ReduceGroup r;
-  load_group(r, a.part_lse + bh * S, a.part_out + bh * S * D + d, D, 0, S);
-  float M = group_max(r);
+  const int np = a.num_partials;
+  ChainRegs r;
+  load_chain(r, a.part_lse + bh * np, a.part_out + bh * np * D + d, D, 0, np);
+  if constexpr (FOLD) {
+    // Level 2 in place: group q's result replaces entry q (q < kChain / 4).
+#pragma unroll
+    for (int q = 0; q < kChain / kSplitGroup; ++q) {
+      GroupFold f;
+      float4 gx = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int k = 0; k < kSplitGroup; ++k) {
+        const int s = q * kSplitGroup + k;
+        float wa, wb;
+        group_fold_weights(f, r.l[s], wa, wb);
+        gx.x = group_fold_value(gx.x, r.x[s].x, wa, wb);
+        gx.y = group_fold_value(gx.y, r.x[s].y, wa, wb);
+        gx.z = group_fold_value(gx.z, r.x[s].z, wa, wb);
+        gx.w = group_fold_value(gx.w, r.x[s].w, wa, wb);
+      }
+      const float inv = group_inv(f);
+      r.l[q] = group_lse(f);
+      r.x[q] = make_float4(gx.x * inv, gx.y * inv, gx.z * inv, gx.w * inv);
+    }
+#pragma unroll
+    for (int q = kChain / kSplitGroup; q < kChain; ++q) {
+      r.l[q] = kNegInf;
+      r.x[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  float M = chain_max(r);
   if (M == kNegInf) M = 0.f;
   float4 num;
   float den;
-  chain_group(r, M, num, den);
+  chain_sums(r, M, num, den);
   store_reduced(a, bh, d, num, den);
 }
 
-// S > kReduceGroup: one work-group per (row, head, 32-dim slice); thread
-// (chunk, q) sums group q of the current set of 32 groups, then the threads of
-// group 0 add the set's group sums in order onto the running total.
+// More than kChain group results per (row, head) (written by the split
+// waves, no folding): one work-group per (row, head, 32-dim slice); thread
+// (chunk, q) sums chain q of the current set of chains, then the threads of
+// chain 0 add the set's chain sums in order onto the running total.
 template <int D>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeArgs a) {
   constexpr int DS = 32;          // dims per work-group
   constexpr int CH = DS / 4;      // float4 chunks per slice
-  constexpr int NQ = 256 / CH;    // groups per set
+  constexpr int NQ = 256 / CH;    // chains per set
   constexpr int SLICES = D / DS;
   __shared__ float red[256];
   __shared__ float4 gnum[NQ][CH];
-  static_assert(NQ <= 256, "max pass scratch");
   __shared__ float gden[NQ];
 
   const int64_t bh = blockIdx.x / SLICES;
   const int d0 = (blockIdx.x % SLICES) * DS;
-  const int S = a.num_splits;
-  const float* lse = a.part_lse + bh * S;
-  const float* po = a.part_out + bh * S * D + d0;
+  const int np = a.num_partials;
+  const float* lse = a.part_lse + bh * np;
+  const float* po = a.part_out + bh * np * D + d0;
 
   const int ch = threadIdx.x % CH;
   const int q = threadIdx.x / CH;
-  ReduceGroup r;
+  ChainRegs r;
   float M;
-  if (S <= NQ * kReduceGroup) {
-    // One set: the group loads double as the max pass.
-    load_group(r, lse, po + 4 * ch, D, q * kReduceGroup, S);
-    if (ch == 0) red[q] = group_max(r);
+  if (np <= NQ * kChain) {
+    // One set: the chain loads double as the max pass.
+    load_chain(r, lse, po + 4 * ch, D, q * kChain, np);
+    if (ch == 0) red[q] = chain_max(r);
     __syncthreads();
     M = kNegInf;
     for (int k = 0; k < NQ; ++k) M = fmaxf(M, red[k]);
   } else {
     M = kNegInf;
-    for (int s = threadIdx.x; s < S; s += 256) M = fmaxf(M, lse[s]);
+    for (int s = threadIdx.x; s < np; s += 256) M = fmaxf(M, lse[s]);
     red[threadIdx.x] = M;
     __syncthreads();
     for (int off = 128; off > 0; off >>= 1) {
@@ -158,11 +183,11 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeArgs a) {
   float4 total = make_float4(0.f, 0.f, 0.f, 0.f);
   float total_den = 0.f;
   bool any = false;
-  for (int set0 = 0; set0 < S; set0 += NQ * kReduceGroup) {
-    if (set0 > 0 || S > NQ * kReduceGroup) load_group(r, lse, po + 4 * ch, D, set0 + q * kReduceGroup, S);
+  for (int set0 = 0; set0 < np; set0 += NQ * kChain) {
+    if (set0 > 0 || np > NQ * kChain) load_chain(r, lse, po + 4 * ch, D, set0 + q * kChain, np);
     float4 num;
     float den;
-    chain_group(r, M, num, den);
+    chain_sums(r, M, num, den);
     gnum[q][ch] = num;
     if (ch == 0) gden[q] = den;
     __syncthreads();
@@ -188,13 +213,67 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeArgs a) {
   if (q == 0) store_reduced(a, bh, d0 + 4 * ch, total, total_den);
 }
 
+// ------------------------------------------------------------ tuning switches
+
+// Process-wide launch choices for experiments and tests (bvllm_set_tuning);
+// none changes results beyond what each knob's comment says.
+static std::atomic<int> g_tuning[kTuneKnobs] = {};
+
+int tuning(int knob) { return (knob >= 0 && knob < kTuneKnobs) ? g_tuning[knob].load(std::memory_order_relaxed) : 0; }
+
+int set_tuning(int knob, int value) {
+  if (knob < 0 || knob >= kTuneKnobs) return -1;
+  return g_tuning[knob].exchange(value, std::memory_order_relaxed);
+}
+
+// ------------------------------------------------------------ the launch plan
+
+// How a decode launch runs (the split boundaries come from the caller's plan):
+//   single pass (one split): work-groups of 4 waves, bf16 output directly;
+//   split, one wave per split ("split" mode): partials per split, level 2 in
+//     the reduce;
+//   split, one wave per group of kSplitGroup splits ("group" mode): level 2 in
+//     the wave, one partial per group.
+// Both split modes give the same bits. Group mode needs bps % 4 == 0 (the
+// group then starts every split on a page index ≡ 0 mod 4 of the wave's
+// stream); split mode folds at most kChain splits in the reduce. The default
+// takes group mode when there are more than kChain splits or enough groups to
+// fill the GPU (2 per CU of a 256-CU MI355X), split mode otherwise.
+DecodePlan decode_plan(int32_t batch, int32_t num_kv_heads, int32_t num_splits, int32_t blocks_per_split) {
+  DecodePlan p{};
+  if (num_splits <= 1) {
+    p.single_pass = true;
+    p.partials = 0;
+    return p;
+  }
+  p.group = (blocks_per_split % kSplitGroup == 0) ? kSplitGroup : 1;
+  const int64_t groups = (num_splits + p.group - 1) / p.group;
+  bool group_mode = p.group > 1 && (num_splits > kChain || (int64_t)batch * num_kv_heads * groups >= 512);
+  const int forced = tuning(kTuneDecodeSplitMode);
+  if (forced == 1 && (p.group == 1 || num_splits <= kChain)) group_mode = false;
+  if (forced == 2 && p.group > 1) group_mode = true;
+  p.splits_per_item = group_mode ? p.group : 1;
+  p.partials = group_mode ? (int32_t)groups : num_splits;
+  p.fold_in_reduce = !group_mode && p.group > 1;
+  return p;
+}
+
+int32_t decode_partials(int32_t batch, int32_t num_kv_heads, int32_t num_splits, int32_t blocks_per_split) {
+  return decode_plan(batch, num_kv_heads, num_splits, blocks_per_split).partials;
+}
+
 template <int D>
-static hipError_t launch_reduce(const DecodeArgs& r, hipStream_t stream) {
-  if (r.num_splits <= kReduceGroup) {
+static hipError_t launch_reduce(const DecodeArgs& r, const DecodePlan& p, hipStream_t stream) {
+  const int64_t groups = p.fold_in_reduce ? (r.num_partials + kSplitGroup - 1) / kSplitGroup : r.num_partials;
+  if (groups <= kChain && (!p.fold_in_reduce || r.num_partials <= kChain)) {
     const int64_t items = (int64_t)r.batch * r.num_heads * (D / 4);
-    hipLaunchKernelGGL((decode_reduce_small_kernel<D>), dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
-                       stream, r, items);
+    const dim3 grid((unsigned)((items + 255) / 256));
+    if (p.fold_in_reduce)
+      hipLaunchKernelGGL((decode_reduce_small_kernel<D, true>), grid, dim3(256), 0, stream, r, items);
+    else
+      hipLaunchKernelGGL((decode_reduce_small_kernel<D, false>), grid, dim3(256), 0, stream, r, items);
   } else {
+    if (p.fold_in_reduce) return hipErrorInvalidValue;  // excluded by decode_plan
     hipLaunchKernelGGL((decode_reduce_kernel<D>), dim3((unsigned)(r.batch * r.num_heads * (D / 32))), dim3(256),
                        0, stream, r);
   }
@@ -215,120 +294,76 @@ int device_cus() {
   return v;
 }
 
-// Consecutive splits per work-group: about two work-groups per compute unit
-// when the plan has more (small splits of a short batch, e.g. 512 splits of 4
-// pages at batch 1: 4 splits per work-group, 33.7 instead of 37.5 us on
-// MI355X), so that each work-group streams several splits' pages back to back.
-// BVLLM_DECODE_SPLITS_PER_WG overrides the choice for tuning.
-static int decode_splits_per_wg(const DecodeArgs& a, int nw) {
-  if (a.num_splits <= 1 || a.blocks_per_split % nw != 0) return 1;
-  const char* env = getenv("BVLLM_DECODE_SPLITS_PER_WG");  // read per launch: tests vary it
-  const int forced = env ? atoi(env) : 0;
-  int64_t gps;
-  if (forced > 0) {
-    gps = forced;
-  } else {
-    const int64_t cus = device_cus();
-    const int64_t total = (int64_t)a.batch * a.num_kv_heads * a.num_splits;
-    gps = (total + cus) / (2 * cus);
+// Sets a kernel's dynamic-LDS limit once per device (setting it twice, from
+// racing host threads, is harmless).
+template <typename K>
+static hipError_t allow_lds(K* kernel, std::atomic<bool> (&done)[64], int bytes) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  if (!done[dev].load(std::memory_order_acquire)) {
+    err = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              bytes);
+    if (err != hipSuccess) return err;
+    done[dev].store(true, std::memory_order_release);
   }
-  return (int)std::max<int64_t>(1, std::min<int64_t>(gps, a.num_splits));
+  return hipSuccess;
 }
 
-// Splits of at most this many pages run one per wave (decode_split_wave):
-// with 4 or 8 pages per split the work-group path spends most of a split in
-// its cross-wave merge. BVLLM_DECODE_SPLIT_WAVES=0 / 1 forces the work-group
-// / the per-wave path for any split plan (read per launch: tests vary it).
-constexpr int kSplitWaveMaxPages = 8;
-static bool use_split_waves(const DecodeArgs& a) {
-  if (a.num_splits <= 1 || a.waves != 4 || a.query_start_loc != nullptr) return false;
-  const char* env = getenv("BVLLM_DECODE_SPLIT_WAVES");
-  if (env && env[0] == '0') return false;
-  if (env && env[0] == '1') return true;
-  return a.blocks_per_split <= kSplitWaveMaxPages;
+template <int D, int PF, bool GROUP>
+static hipError_t launch_stream_pf(const DecodeArgs& a, int64_t items, hipStream_t stream) {
+  if (tuning(kTuneDecodeCached) == 0)
+    hipLaunchKernelGGL((paged_decode_stream_kernel<D, PF, true, GROUP>), dim3((unsigned)items), dim3(64), 0,
+                       stream, a, (int)items);
+  else
+    hipLaunchKernelGGL((paged_decode_stream_kernel<D, PF, false, GROUP>), dim3((unsigned)items), dim3(64), 0,
+                       stream, a, (int)items);
+  return hipGetLastError();
+}
+
+// Two pages in flight per streaming wave. (Four do not fit the register file
+// next to the four states: the compiler then parks registers that in-flight
+// loads still write.)
+template <int D, bool GROUP>
+static hipError_t launch_stream(const DecodeArgs& a, int64_t items, hipStream_t stream) {
+  return launch_stream_pf<D, 2, GROUP>(a, items, stream);
 }
 
 template <int D>
-static hipError_t launch_split_waves(const DecodeArgs& a, hipStream_t stream) {
-  const int64_t items = (int64_t)a.batch * a.num_kv_heads * a.num_splits;
-  if (items == 0) return hipSuccess;
-  if (items > 0x7ffffff0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((paged_decode_split_wave_kernel<D, 2>), dim3((unsigned)items), dim3(64), 0, stream, a,
-                     (int)items);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  return launch_reduce<D>(a, stream);
-}
-
-template <int D, int NW, int PF>
 static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
   DecodeArgs a = args;
-  if (use_split_waves(a)) return launch_split_waves<D>(a, stream);
-  a.splits_per_wg = decode_splits_per_wg(a, NW);
-  const int G = a.num_heads / a.num_kv_heads;
-  const size_t smem = decode_lds_bytes<D, NW>(G);
-  if (smem > 160 * 1024) return hipErrorInvalidValue;
-  // The dynamic-LDS limit is a per-device function attribute: set once per
-  // device (setting it twice, from racing host threads, is harmless).
-  static std::atomic<bool> attr_set[64] = {};
-  int dev = 0;
-  hipError_t de = hipGetDevice(&dev);
-  if (de != hipSuccess) return de;
-  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-  if (!attr_set[dev].load(std::memory_order_acquire)) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_decode_kernel<D, NW, PF>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) return e;
-    attr_set[dev].store(true, std::memory_order_release);
+  const DecodePlan p = decode_plan(a.batch, a.num_kv_heads, a.num_splits, a.blocks_per_split);
+  a.item_order = tuning(kTuneDecodeOrder) == 1 ? 1 : 0;
+  if (p.single_pass && tuning(kTuneDecodeSinglePassStream) == 0) {
+    constexpr int NW = 4;
+    const int G = a.num_heads / a.num_kv_heads;
+    const size_t smem = decode_lds_bytes<D, NW>(G);
+    if (smem > 160 * 1024) return hipErrorInvalidValue;
+    static std::atomic<bool> done[64] = {};
+    hipError_t err = allow_lds(&paged_decode_kernel<D, NW, 2>, done, 160 * 1024);
+    if (err != hipSuccess) return err;
+    const int64_t wgs = (int64_t)a.batch * a.num_kv_heads;
+    if (wgs > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((paged_decode_kernel<D, NW, 2>), dim3((unsigned)wgs), dim3(NW * 64), smem, stream, a);
+    return hipGetLastError();
   }
-  const int64_t groups = (a.num_splits + a.splits_per_wg - 1) / a.splits_per_wg;
-  const int64_t wgs = (int64_t)a.batch * a.num_kv_heads * groups;
-  if (wgs == 0) return hipSuccess;
-  if (wgs > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((paged_decode_kernel<D, NW, PF>), dim3((unsigned)wgs), dim3(NW * 64), smem, stream, a);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess || a.num_splits == 1) return err;
-  return launch_reduce<D>(a, stream);
+  a.splits_per_item = p.single_pass ? 1 : p.splits_per_item;
+  a.num_partials = p.partials;
+  const int64_t units = (a.num_splits + a.splits_per_item - 1) / a.splits_per_item;
+  const int64_t items = (int64_t)a.batch * a.num_kv_heads * units;
+  if (items > 0x7ffffff0) return hipErrorInvalidValue;
+  hipError_t err = a.splits_per_item > 1 ? launch_stream<D, true>(a, items, stream)
+                                         : launch_stream<D, false>(a, items, stream);
+  if (err != hipSuccess || p.single_pass) return err;
+  return launch_reduce<D>(a, p, stream);
 }
-
-// Pages in flight per wave; BVLLM_DECODE_DEPTH (2, 3 or 4) overrides the default for tuning.
-// Two is best measured on MI355X: deeper queues lose DRAM efficiency on the
-// 256-byte head slices.
-static int decode_depth() {
-  static const int depth = [] {
-    const char* e = getenv("BVLLM_DECODE_DEPTH");
-    const int v = e ? atoi(e) : 0;
-    return (v >= 2 && v <= 4) ? v : 2;
-  }();
-  return depth;
-}
-
-template <int D, int NW>
-static hipError_t decode_for_depth(const DecodeArgs& a, hipStream_t stream) {
-  switch (decode_depth()) {
-    case 2: return launch_decode<D, NW, 2>(a, stream);
-    case 4: return launch_decode<D, NW, 4>(a, stream);
-    default: return launch_decode<D, NW, 3>(a, stream);
-  }
-}
-
-template <int D>
-static hipError_t decode_for_dim(const DecodeArgs& a, hipStream_t stream) {
-  switch (a.waves) {
-    case 4: return decode_for_depth<D, 4>(a, stream);
-    case 8: return decode_for_depth<D, 8>(a, stream);
-    default: return hipErrorInvalidValue;
-  }
-}
-
-int32_t decode_partials(const DecodeArgs& a) { return a.num_splits; }
 
 hipError_t paged_decode(const DecodeArgs& a, hipStream_t stream) {
-  DecodeArgs d = a;
-  if (d.waves == 0) d.waves = 4;
+  if (a.waves != 0 && a.waves != 4) return hipErrorInvalidValue;
   switch (a.head_dim) {
-    case 64: return decode_for_dim<64>(d, stream);
-    case 128: return decode_for_dim<128>(d, stream);
+    case 64: return launch_decode<64>(a, stream);
+    case 128: return launch_decode<128>(a, stream);
     default: return hipErrorInvalidValue;
   }
 }

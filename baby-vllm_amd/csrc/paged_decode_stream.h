@@ -1,0 +1,283 @@
+// Split (flash-decoding) paged decode on streaming waves, and the split merge.
+//
+// Replaces paged_decode_attn_split_kernel (babyvllm/kernels/paged_attn.py:104-213).
+// A split of the plan covers pages [s·bps, (s+1)·bps) of its row (the last
+// split runs to the row's last page). One wave computes one split, or a group
+// of consecutive splits, as a stream of pages:
+//
+//   * Pages come into registers by 16-byte loads of whole 256-byte row slices
+//     (the work-group path's page loads), PF pages in flight: page k + PF is
+//     requested as soon as page k is consumed; K passes through the wave's
+//     transpose tile into the MFMA layout, V is used from registers.
+//     (Measured and rejected: staging pages in LDS by direct global -> LDS
+//     loads, whose issue took a wave 3.4 us for 8 pages at batch 8; and batches
+//     of four pages computed as one block, which do not fit the register file
+//     next to the four states and the pages in flight.)
+//   * A split keeps the 4 online-softmax states of a single-pass work-group
+//     (state s takes the split's pages start+s, start+s+4, ...) and merges them
+//     with merge_states' arithmetic, so a split's (o, lse) has the bits of the
+//     work-group path and a row within one split matches the single pass.
+//
+// Split results are merged in two fixed levels, the same arithmetic wherever
+// they run, so neither the launch shape nor the bucket changes the bits:
+//   level 2: groups of kSplitGroup consecutive splits (when bps % 4 == 0; else
+//            groups of one) fold their splits in order (GroupFold);
+//   level 3: the decode reduce chains the group results (paged_decode.hip).
+// Level 2 runs in the streaming wave when one wave computes a whole group (the
+// plans with many splits: one partial per group is written, a quarter of the
+// partial traffic), and in the reduce otherwise (few splits: one wave per
+// split spreads a short batch over every CU). Empty splits (no live page)
+// leave a group unchanged, and empty groups add nothing in level 3, so a graph
+// launch sized for a longer bucket gives the bits of a launch sized for the
+// live length.
+#pragma once
+
+#include "paged_decode_wg.h"
+
+#include <climits>
+
+namespace bvllm {
+
+// Consecutive splits folded into one partial (level 2) when the plan's
+// pages per split is a multiple of 4.
+constexpr int kSplitGroup = 4;
+
+// Level 2: folds the (o, lse) of a group's splits, in split order, into a
+// running (M, L, A) with the online rescale: M' = max(M, lse), A = A·2^(M−M')
+// + o·2^(lse−M'), L = L·2^(M−M') + 2^(lse−M'); the group's result is
+// o = A · (1 / L), lse = M + log2 L (o = 0, lse = −inf when every split is
+// empty). Folding an empty split (lse = −inf, o = 0) leaves (M, L, A)
+// bit-identical, and a group with one non-empty split yields exactly that
+// split's (o, lse).
+struct GroupFold {
+  float M = kNegInf;
+  float L = 0.f;
+};
+__device__ __forceinline__ void group_fold_weights(GroupFold& f, float lse, float& wa, float& wb) {
+  const float Mn = fmaxf(f.M, lse);
+  if (Mn == kNegInf) {  // nothing live yet: stays empty
+    wa = 1.f;
+    wb = 0.f;
+    return;
+  }
+  wa = fast_exp2(f.M - Mn);
+  wb = fast_exp2(lse - Mn);
+  f.L = __builtin_fmaf(f.L, wa, wb);
+  f.M = Mn;
+}
+__device__ __forceinline__ float group_fold_value(float acc, float x, float wa, float wb) {
+  return __builtin_fmaf(x, wb, acc * wa);
+}
+__device__ __forceinline__ float group_inv(const GroupFold& f) { return f.L > 0.f ? 1.f / f.L : 0.f; }
+__device__ __forceinline__ float group_lse(const GroupFold& f) { return f.L > 0.f ? f.M + __log2f(f.L) : kNegInf; }
+
+// One streaming decode wave: item = (row, KV head, unit of a.splits_per_item
+// consecutive splits); `tile` is the wave's K transpose tile (kTileBytes<D>
+// bytes of LDS).
+template <int D, int PF, bool NT, bool GROUP>
+__device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const int item, unsigned char* tile) {
+  constexpr int KC = D / 32;
+  constexpr int VD = D / 16;
+  constexpr int OPL = D / 4;  // output floats per lane: head n, dims VD·(4g+i) + c
+  static_assert(PF == 2, "pages in flight per wave");
+
+  const int G = a.num_heads / a.num_kv_heads;
+  const int S = a.num_splits;
+  const int spi = GROUP ? a.splits_per_item : 1;
+  const int units = (S + spi - 1) / spi;
+  int kvh, unit, b;
+  if (a.item_order == 0) {  // KV head fastest: the 4 head slices of a page are requested together
+    kvh = item % a.num_kv_heads;
+    const int rest = item / a.num_kv_heads;
+    unit = rest % units;
+    b = rest / units;
+  } else {  // unit fastest
+    unit = item % units;
+    const int rest = item / units;
+    kvh = rest % a.num_kv_heads;
+    b = rest / a.num_kv_heads;
+  }
+  const int j0 = unit * spi;
+  const int j1 = min(j0 + spi, S);
+  const int bps = a.blocks_per_split;
+  const int p0 = j0 * bps;
+
+  const int lane = lane_id();
+  const int n = lane & 15;
+  const int g = lane >> 4;
+
+  // The table slice, seq_len and q are requested together (the slice index is
+  // clamped into the row, so it does not wait for seq_len).
+  const int32_t* bt = a.block_tables + (int64_t)b * a.bt_stride;
+  int ent = bt[min(p0 + lane, a.max_blocks - 1)];
+  const int seq_len = uniform(a.seq_lens[b]);
+  uint4 qb[KC];
+  {
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_sb +
+                           (int64_t)(kvh * G + n) * a.q_sh;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) qb[c] = (n < G) ? ld16(qrow + 8 * (4 * c + g)) : make_uint4(0, 0, 0, 0);
+  }
+  int n_blocks = seq_len > 0 ? (seq_len + 15) / 16 : 0;
+  n_blocks = min(n_blocks, a.max_blocks);
+  // The last split of the row runs to the row's last page.
+  const int p_end = (j1 == S) ? n_blocks : min(j1 * bps, n_blocks);
+  const int cnt = max(p_end - p0, 0);
+
+  uint32_t off[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) off[j] = (uint32_t)((4 * g + j) * a.c_st + VD * n);
+  const uint16_t* kc = reinterpret_cast<const uint16_t*>(a.k_cache) + (int64_t)kvh * a.c_sh;
+  const uint16_t* vc = reinterpret_cast<const uint16_t*>(a.v_cache) + (int64_t)kvh * a.c_sh;
+
+  WaveState<D> st[4];
+  auto reset = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      st[s].m = kNegInf;
+      st[s].l = 0.f;
+#pragma unroll
+      for (int c = 0; c < VD; ++c) st[s].acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  reset();
+
+  // Group accumulator (level 2 in the wave; group waves only).
+  float go[GROUP ? OPL : 1];
+#pragma unroll
+  for (int k = 0; k < (GROUP ? OPL : 1); ++k) go[k] = 0.f;
+  GroupFold gf;
+
+  const int64_t head = (int64_t)kvh * G + n;
+  // Merges the 4 states of split `split` (merge_states' arithmetic, per lane)
+  // and folds or writes its (o, lse).
+  auto finish_split = [&](int split) __attribute__((always_inline)) {
+    float lt[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) lt[s] = sum_across_groups(st[s].l);
+    float M = kNegInf;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) M = fmaxf(M, st[s].m);
+    float L = 0.f;
+    float o[OPL];
+#pragma unroll
+    for (int k = 0; k < OPL; ++k) o[k] = 0.f;
+    if (M != kNegInf) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float wgt = fast_exp2(st[s].m - M);
+        L = __builtin_fmaf(lt[s], wgt, L);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int c = 0; c < VD; ++c) o[VD * i + c] = __builtin_fmaf(st[s].acc[c][i], wgt, o[VD * i + c]);
+      }
+    }
+    const float inv = split_inv(L);
+#pragma unroll
+    for (int k = 0; k < OPL; ++k) o[k] = L == 0.f ? 0.f : o[k] * inv;
+    const float lse = split_lse(M, L);
+    if constexpr (GROUP) {
+      float wa, wb;
+      group_fold_weights(gf, lse, wa, wb);
+#pragma unroll
+      for (int k = 0; k < OPL; ++k) go[k] = group_fold_value(go[k], o[k], wa, wb);
+    } else if (n < G) {
+      if (S == 1) {
+        uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)b * a.o_sb + head * a.o_sh;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (VD == 8) {
+            uint4 pk;
+            pk.x = pack_bf16x2_hw(o[VD * i + 0], o[VD * i + 1]);
+            pk.y = pack_bf16x2_hw(o[VD * i + 2], o[VD * i + 3]);
+            pk.z = pack_bf16x2_hw(o[VD * i + 4], o[VD * i + 5]);
+            pk.w = pack_bf16x2_hw(o[VD * i + 6], o[VD * i + 7]);
+            st16(dst + VD * (4 * g + i), pk);
+          } else {
+            uint2 pk;
+            pk.x = pack_bf16x2_hw(o[VD * i + 0], o[VD * i + 1]);
+            pk.y = pack_bf16x2_hw(o[VD * i + 2], o[VD * i + 3]);
+            st8(dst + VD * (4 * g + i), pk);
+          }
+        }
+      } else {
+        const int64_t prow = ((int64_t)b * a.num_heads + head) * a.num_partials + split;
+        float* dst = a.part_out + prow * D;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int c = 0; c < VD; c += 4)
+            *reinterpret_cast<float4*>(dst + VD * (4 * g + i) + c) =
+                make_float4(o[VD * i + c], o[VD * i + c + 1], o[VD * i + c + 2], o[VD * i + c + 3]);
+        if (g == 0) a.part_lse[prow] = lse;
+      }
+    }
+    reset();
+  };
+
+  int cur = j0;  // split whose states are open
+  // Item-relative page index where split cur + 1 starts (none past the unit).
+  int next_start = (cur + 1 < j1) ? bps : INT_MAX;
+  bool any = false;  // a page of split cur was processed
+
+  // Pages are taken four at a time (page k + i into state i), PF in flight;
+  // loads are issued for clamped page indices (in bounds), and pages past the
+  // chunk's end are skipped (a fully masked page would leave its state
+  // bit-identical anyway).
+  for (int base = 0; base < cnt; base += 64) {
+    const int here = min(64, cnt - base);
+    if (base > 0) ent = bt[min(p0 + base + lane, a.max_blocks - 1)];
+    const int slot_ent = min(max(ent, 0), a.num_pages - 1);
+    auto phys = [&](int k) -> int64_t { return (int64_t)__builtin_amdgcn_readlane(slot_ent, k); };
+    PageRegs<D> r[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int64_t p = phys(min(i, here - 1)) * a.c_sb;
+      load_page<D, NT>(r[i], kc + p, vc + p, off);
+    }
+    for (int k = 0; k < here; k += 4) {
+      if constexpr (GROUP) {
+        if (base + k == next_start) {  // a new split of the unit starts at this page
+          finish_split(cur);
+          ++cur;
+          next_start = (cur + 1 < j1) ? next_start + bps : INT_MAX;
+          any = false;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        wait_page<(PF - 1) * kLoadsPerPage, D>(r[i % PF]);
+        const int page = p0 + base + k + i;
+        if (k + i < here)
+          process_page<D>(st[i], r[i % PF], qb, tile, n, g, page * 16 + 4 * g, seq_len, a.scale_log2);
+        const int64_t pn = phys(min(k + i + PF, here - 1)) * a.c_sb;
+        load_page<D, NT>(r[i % PF], kc + pn, vc + pn, off);
+      }
+      any = true;
+    }
+    // Drain: the loads issued past the end must land before their registers
+    // are reused.
+#pragma unroll
+    for (int i = 0; i < PF; ++i) wait_page<0, D>(r[i]);
+  }
+  // The split holding the unit's last pages (for a unit of one split, also
+  // when it has no page: its partial is written as empty).
+  if (any || !GROUP) finish_split(cur);
+
+  if (GROUP && n < G) {
+    const int64_t prow = ((int64_t)b * a.num_heads + head) * a.num_partials + unit;
+    float* dst = a.part_out + prow * D;
+    const float ginv = group_inv(gf);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int c = 0; c < VD; c += 4)
+        *reinterpret_cast<float4*>(dst + VD * (4 * g + i) + c) =
+            make_float4(go[VD * i + c] * ginv, go[VD * i + c + 1] * ginv, go[VD * i + c + 2] * ginv,
+                        go[VD * i + c + 3] * ginv);
+    if (g == 0) a.part_lse[prow] = group_lse(gf);
+  }
+}
+
+}  // namespace bvllm

@@ -2,18 +2,17 @@
 // (paged_decode.hip) and the prefill kernel, which runs the single-query
 // sequences of a mixed step with it.
 //
-// Paged decode attention: one query token per sequence against its paged K/V,
-// with the flash-decoding split (partial softmax per split + LSE reduce).
+// Replaces paged_decode_attn_kernel (babyvllm/kernels/paged_attn.py:9-101),
+// the single-pass decode; the page math (page_scores, page_softmax_pv) is
+// shared with the split launches.
 //
-// Replaces paged_decode_attn_kernel, paged_decode_attn_split_kernel and
-// paged_decode_attn_reduce_kernel (babyvllm/kernels/paged_attn.py:9-251).
-//
-// Work-group = (sequence b, KV head, split). Its NW waves walk the split's
-// pages interleaved (wave w takes pages start+w, start+w+NW, ...), each with a
-// private online-softmax state, and merge the NW states in LDS in wave order.
-// The page→wave assignment depends only on the split's first page and NW, so
-// a row that fits in one split gives the same bits whether the launch is the
-// single-pass one (one split) or a split one.
+// Work-group = (sequence b, KV head) of a single-pass launch. Its NW = 4 waves
+// walk the row's pages interleaved (wave w takes pages w, w+4, ...), each with
+// a private online-softmax state, and merge the 4 states in LDS in wave order.
+// The split launches (paged_decode_stream.h) keep the same 4 states per split
+// (state s takes the split's pages start+s, start+s+4, ...) and merge them
+// with the same arithmetic, so a row that fits in one split gives the same
+// bits from the single-pass launch and from a split launch.
 //
 // Loads: a page of one KV head is 16 token rows of D·2 bytes at a 1 KB stride
 // (7B shape). Both K and V are fetched as 4 whole rows per instruction (lane
@@ -64,20 +63,25 @@ struct PageRegs {
 // The loads carry the nontemporal hint: each KV byte is read once per call, and
 // streaming it past the caches lifts the read rate of this access pattern by
 // about 12% on MI355X (6.37 vs 5.61 TB/s measured without compute).
-template <int D>
+template <int D, bool NT = true>
 __device__ __forceinline__ void gload(RowSlice<D>& r, const uint16_t* base, uint32_t off_elems) {
   const uint32_t off = off_elems * 2;
-  if constexpr (D / 16 == 8) asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(r) : "v"(off), "s"(base));
-  else asm volatile("global_load_dwordx2 %0, %1, %2 nt" : "=v"(r) : "v"(off), "s"(base));
+  if constexpr (NT) {
+    if constexpr (D / 16 == 8) asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(r) : "v"(off), "s"(base));
+    else asm volatile("global_load_dwordx2 %0, %1, %2 nt" : "=v"(r) : "v"(off), "s"(base));
+  } else {
+    if constexpr (D / 16 == 8) asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(r) : "v"(off), "s"(base));
+    else asm volatile("global_load_dwordx2 %0, %1, %2" : "=v"(r) : "v"(off), "s"(base));
+  }
 }
 
-template <int D>
+template <int D, bool NT = true>
 __device__ __forceinline__ void load_page(PageRegs<D>& r, const uint16_t* kbase, const uint16_t* vbase,
                                           const uint32_t (&off)[4]) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) gload<D>(r.k[j], kbase, off[j]);
+  for (int j = 0; j < 4; ++j) gload<D, NT>(r.k[j], kbase, off[j]);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) gload<D>(r.v[j], vbase, off[j]);
+  for (int j = 0; j < 4; ++j) gload<D, NT>(r.v[j], vbase, off[j]);
 }
 
 constexpr int kLoadsPerPage = 8;
@@ -97,24 +101,43 @@ struct WaveState {
   f32x4_t acc[D / 16];  // acc[c][i] = O[head][(D/16)·(4g+i) + c]
 };
 
-// One page of the online softmax. Tokens at or past tok_limit are masked: their
-// scores become -inf and their V rows are replaced by zeros where they are used
-// (unwritten slots may hold NaN, and 0·NaN would poison the PV product). The
-// masking is branch-free so that the loads of the pages in flight stay in flight.
+// Sᵀ of one page: the D/32 MFMAs of K·Qᵀ in k-step order, from the K operand
+// chunks kop[c] = K row n, dims 8(4c+g) .. +8 (lane n + 16g). Every page path
+// (K through a transpose tile or straight from a staged page in LDS) forms
+// the same operands and the same chain, so its scores have the same bits.
 template <int D>
-__device__ __forceinline__ void process_page(WaveState<D>& st, const PageRegs<D>& r, const uint4 (&qb)[D / 32],
-                                             unsigned char* tile, int n, int g,
-                                             int tok0, int tok_limit, float scale_log2) {
-  constexpr int VD = D / 16;
-  constexpr int PITCH = 2 * D + 16;  // bytes; the pad keeps 16-row column reads conflict-free
-#pragma unroll
-  for (int j = 0; j < 4; ++j) *reinterpret_cast<RowSlice<D>*>(tile + (4 * g + j) * PITCH + 2 * VD * n) = r.k[j];
-  asm volatile("" ::: "memory");
+__device__ __forceinline__ f32x4_t page_scores(const uint4 (&kop)[D / 32], const uint4 (&qb)[D / 32]) {
   f32x4_t s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int c = 0; c < D / 32; ++c) s = mfma_16x16x32(ld16(tile + n * PITCH + 16 * (4 * c + g)), qb[c], s);
-  asm volatile("" ::: "memory");
+  for (int c = 0; c < D / 32; ++c) s = mfma_16x16x32(kop[c], qb[c], s);
+  return s;
+}
 
+// The online softmax and PV product of one page, from its scores s (lane
+// n + 16g holds S[head n][token 4g+i]) and its V rows v[j] = V row 4g+j, dims
+// (D/16)·n .. +D/16, in three phases so that a wave with several independent
+// states can interleave their pages (a dependent VALU operation waits about
+// 36 clocks for its operand on gfx950, so one page alone is latency-bound):
+//   softmax_phase: scores, running max and sum, P, and the PV operands;
+//   rescale_phase: the accumulator rescale, skipped when alpha is 1 on every
+//                  lane (x·1 == x: skipping is exact);
+//   pv_phase:      the PV MFMAs.
+// Tokens at or past tok_limit are masked: their scores become -inf and their
+// V rows are replaced by zeros where they are used (unwritten slots may hold
+// NaN, and 0·NaN would poison the PV product). The masking is branch-free so
+// that loads in flight stay in flight.
+template <int D>
+struct PagePv {
+  float alpha;
+  uint2 pb;            // P, bf16, B operand of the PV MFMAs
+  uint2 va[D / 16];    // V^T operands (row = dim (D/16)·r + c, k = token 4g+i)
+};
+
+template <int D>
+__device__ __forceinline__ void softmax_phase(WaveState<D>& st, PagePv<D>& ph, f32x4_t s,
+                                              const RowSlice<D> (&v)[4], int tok0, int tok_limit,
+                                              float scale_log2) {
+  constexpr int VD = D / 16;
   bool live[4];
   float sv[4];
 #pragma unroll
@@ -130,34 +153,68 @@ __device__ __forceinline__ void process_page(WaveState<D>& st, const PageRegs<D>
   // e.g. a padding page that opens a split's state) 0 stands in for the max,
   // so that alpha and p are 0 instead of exp2(-inf - -inf) = NaN.
   const float m_ref = m_new == kNegInf ? 0.f : m_new;
-  const float alpha = fast_exp2(st.m - m_ref);
+  ph.alpha = fast_exp2(st.m - m_ref);
   float p[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) p[i] = fast_exp2(sv[i] - m_ref);
-  st.l = st.l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+  st.l = __builtin_fmaf(st.l, ph.alpha, (p[0] + p[1]) + (p[2] + p[3]));
   st.m = m_new;
-  if (!wave_all_one(alpha)) {  // x·1 == x: skipping is exact
-#pragma unroll
-    for (int c = 0; c < VD; ++c) st.acc[c] *= alpha;
-  }
-
-  uint2 pb;
-  pb.x = pack_bf16x2_hw(p[0], p[1]);
-  pb.y = pack_bf16x2_hw(p[2], p[3]);
+  ph.pb.x = pack_bf16x2_hw(p[0], p[1]);
+  ph.pb.y = pack_bf16x2_hw(p[2], p[3]);
   constexpr int VW = VD / 2;  // dwords per V row slice
   uint32_t vv[4][VW];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
 #pragma unroll
-    for (int x = 0; x < VW; ++x) vv[j][x] = live[j] ? r.v[j][x] : 0u;
+    for (int x = 0; x < VW; ++x) vv[j][x] = live[j] ? v[j][x] : 0u;
   }
 #pragma unroll
   for (int c = 0; c < VD; ++c) {
-    uint2 va;
-    va.x = pick_halves(vv[0][c / 2], vv[1][c / 2], c & 1);
-    va.y = pick_halves(vv[2][c / 2], vv[3][c / 2], c & 1);
-    st.acc[c] = mfma_16x16x16(va, pb, st.acc[c]);
+    ph.va[c].x = pick_halves(vv[0][c / 2], vv[1][c / 2], c & 1);
+    ph.va[c].y = pick_halves(vv[2][c / 2], vv[3][c / 2], c & 1);
   }
+}
+
+template <int D>
+__device__ __forceinline__ void rescale_phase(WaveState<D>& st, const PagePv<D>& ph) {
+  if (!wave_all_one(ph.alpha)) {
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) st.acc[c] *= ph.alpha;
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void pv_phase(WaveState<D>& st, const PagePv<D>& ph) {
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) st.acc[c] = mfma_16x16x16(ph.va[c], ph.pb, st.acc[c]);
+}
+
+template <int D>
+__device__ __forceinline__ void page_softmax_pv(WaveState<D>& st, f32x4_t s, const RowSlice<D> (&v)[4],
+                                                int tok0, int tok_limit, float scale_log2) {
+  PagePv<D> ph;
+  softmax_phase<D>(st, ph, s, v, tok0, tok_limit, scale_log2);
+  rescale_phase<D>(st, ph);
+  pv_phase<D>(st, ph);
+}
+
+// One page from registers (the work-group path): K passes through the wave's
+// transpose tile into the MFMA layout.
+template <int D>
+__device__ __forceinline__ void process_page(WaveState<D>& st, const PageRegs<D>& r, const uint4 (&qb)[D / 32],
+                                             unsigned char* tile, int n, int g,
+                                             int tok0, int tok_limit, float scale_log2) {
+  constexpr int VD = D / 16;
+  constexpr int PITCH = 2 * D + 16;  // bytes; the pad keeps 16-row column reads conflict-free
+#pragma unroll
+  for (int j = 0; j < 4; ++j) *reinterpret_cast<RowSlice<D>*>(tile + (4 * g + j) * PITCH + 2 * VD * n) = r.k[j];
+  asm volatile("" ::: "memory");
+  uint4 kop[D / 32];
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c) kop[c] = ld16(tile + n * PITCH + 16 * (4 * c + g));
+  const f32x4_t s = page_scores<D>(kop, qb);
+  asm volatile("" ::: "memory");
+  page_softmax_pv<D>(st, s, r.v, tok0, tok_limit, scale_log2);
 }
 
 // Bytes of one wave's K transpose tile: 16 rows of D bf16 + 16 bytes of pad.
@@ -184,13 +241,22 @@ __device__ __forceinline__ void save_state(float* rec, const WaveState<D>& st, f
   }
 }
 
-// Merges the NS wave states of one split in wave order (record s at
-// rec + s·rec_stride) and writes the bf16 output row (one split) or the split's
-// fp32 partial output and LSE. Thread `tid` of `nthreads` handles 4
-// consecutive dims of one head at a time.
+// Merge arithmetic of NS per-state results of one split, in state order:
+// M = max of the states' maxima; L and A are fma chains in state order of the
+// states' sums and accumulators weighted by 2^(m_s − M); o = A · (1 / L), or 0
+// when no token was live (L = 0); lse = M + log2 L (−inf when L = 0). Every
+// decode path merges a split's states with these functions (from LDS records
+// in the work-group, from registers in the streaming wave), so a split's
+// (o, lse) has the same bits whichever path computed it.
+__device__ __forceinline__ float split_inv(float L) { return L > 0.f ? 1.f / L : 0.f; }
+__device__ __forceinline__ float split_lse(float M, float L) { return L > 0.f ? M + __log2f(L) : kNegInf; }
+
+// Merges the NS wave states of the row (one split: the single-pass launch) in
+// wave order (record s at rec + s·rec_stride) and writes the bf16 output row.
+// Thread `tid` of `nthreads` handles 4 consecutive dims of one head at a time.
 template <int D, int NS>
-__device__ __forceinline__ void merge_states(const DecodeArgs& a, const float* rec, int rec_stride, int G, int b,
-                                             int row, int kvh, int split, int tid, int nthreads) {
+__device__ __forceinline__ void merge_states(const DecodeArgs& a, const float* rec, int rec_stride, int G,
+                                             int row, int kvh, int tid, int nthreads) {
   const int total4 = G * D / 4;
   for (int e = tid; e < total4; e += nthreads) {
     const int h = (e * 4) / D;
@@ -213,21 +279,15 @@ __device__ __forceinline__ void merge_states(const DecodeArgs& a, const float* r
         A.w = __builtin_fmaf(x.w, wgt, A.w);
       }
     }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const float inv = split_inv(L);
     float4 o = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
     if (L == 0.f) o = make_float4(0.f, 0.f, 0.f, 0.f);
     const int head = kvh * G + h;
-    if (a.num_splits == 1) {
-      uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)row * a.o_sb + (int64_t)head * a.o_sh + d;
-      uint2 pk;
-      pk.x = pack_bf16x2_hw(o.x, o.y);
-      pk.y = pack_bf16x2_hw(o.z, o.w);
-      st8(dst, pk);
-    } else {
-      const int64_t prow = ((int64_t)b * a.num_heads + head) * a.num_splits + split;
-      *reinterpret_cast<float4*>(a.part_out + prow * D + d) = o;
-      if (d == 0) a.part_lse[prow] = (L > 0.f) ? M + __log2f(L) : kNegInf;
-    }
+    uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)row * a.o_sb + (int64_t)head * a.o_sh + d;
+    uint2 pk;
+    pk.x = pack_bf16x2_hw(o.x, o.y);
+    pk.y = pack_bf16x2_hw(o.z, o.w);
+    st8(dst, pk);
   }
 }
 
@@ -238,29 +298,18 @@ constexpr size_t decode_lds_bytes(int G) {
   return (size_t)NW * kTileBytes<D> + (size_t)NW * (32 + G * D) * sizeof(float);
 }
 
-// One decode work-group: (sequence, KV head, group of a.splits_per_wg
-// consecutive splits) = wg, with NW waves and `smem` pointing at
-// decode_lds_bytes<D, NW>(G) bytes of LDS. Each split's state is computed
-// exactly as a work-group of its own would (waves interleave the split's pages
-// from its first page, merge in wave order), so the bits do not depend on
-// splits_per_wg; the pages of the group's next split are already in flight
-// while a split is merged. splits_per_wg > 1 requires blocks_per_split % NW == 0,
-// so that wave w's pages of consecutive full splits continue one progression
-// (first page + w, stride NW) and all waves finish a full split together.
+// One single-pass decode work-group: (sequence, KV head) = wg, with NW waves
+// and `smem` pointing at decode_lds_bytes<D, NW>(G) bytes of LDS. Wave w walks
+// the row's pages w, w + NW, ... with PF pages in flight; the NW states are
+// merged in wave order and the bf16 output row is written.
 template <int D, int NW, int PF>
 __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int wg, float* smem) {
   constexpr int KC = D / 32;
   constexpr int VD = D / 16;
 
   const int G = a.num_heads / a.num_kv_heads;
-  const int gps = a.splits_per_wg;
-  const int n_groups = (a.num_splits + gps - 1) / gps;
-  const int grp = wg % n_groups;
-  const int bk = wg / n_groups;
-  const int kvh = bk % a.num_kv_heads;
-  const int b = bk / a.num_kv_heads;
-  const int j0 = grp * gps;
-  const int j1 = min(j0 + gps, a.num_splits);  // splits [j0, j1)
+  const int kvh = wg % a.num_kv_heads;
+  const int b = wg / a.num_kv_heads;
 
   const int lane = lane_id();
   const int n = lane & 15;
@@ -278,11 +327,6 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
   }
   int n_blocks = seq_len > 0 ? (seq_len + 15) / 16 : 0;
   n_blocks = min(n_blocks, a.max_blocks);
-  const int bps = a.blocks_per_split;
-  const int start = j0 * bps;
-  // The last split of the row runs to the row's last page.
-  const int end = (j1 == a.num_splits) ? n_blocks : min(j1 * bps, n_blocks);
-  const int ppw = bps / NW;  // pages of a full split per wave (splits_per_wg > 1)
 
   // Qᵀ operand: lane (n + 16g), chunk c -> q[b][kvh·G + n][8(4c+g) .. +8).
   uint4 qb[KC];
@@ -294,26 +338,10 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
   }
 
   WaveState<D> st;
-  auto reset = [&]() {
-    st.m = kNegInf;
-    st.l = 0.f;
+  st.m = kNegInf;
+  st.l = 0.f;
 #pragma unroll
-    for (int c = 0; c < VD; ++c) st.acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  };
-  reset();
-
-  // Merge records (m[16], l[16], acc[G][D] per wave) follow the NW K tiles.
-  const int wstride = 32 + G * D;
-  float* merge = smem + NW * kTileBytes<D> / 4;
-  // Merges the NW wave states of split j in wave order and writes its result.
-  // Every wave calls it the same number of times.
-  auto finish_split = [&](int j) {
-    save_state<D>(merge + w * wstride, st, sum_across_groups(st.l), G, n, g);
-    __syncthreads();
-    merge_states<D, NW>(a, merge, wstride, G, b, row, kvh, j, threadIdx.x, NW * 64);
-    __syncthreads();  // records are rewritten by the next split
-    reset();
-  };
+  for (int c = 0; c < VD; ++c) st.acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   uint32_t off[4];
 #pragma unroll
@@ -324,9 +352,8 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
   const uint16_t* vc = reinterpret_cast<const uint16_t*>(a.v_cache) + (int64_t)kvh * a.c_sh;
   const int32_t* bt = a.block_tables + (int64_t)b * a.bt_stride;
 
-  const int first = start + w;
-  const int cnt = (end > first) ? (end - first + NW - 1) / NW : 0;
-  int j_cur = j0;  // split the wave state belongs to
+  const int first = w;
+  const int cnt = (n_blocks > first) ? (n_blocks - first + NW - 1) / NW : 0;
   // Lane k holds the table entry of this wave's page number base + k. The first
   // slice is requested together with seq_len and q (its index is clamped into
   // the row, so it does not wait for seq_len); entries past the row are unused.
@@ -352,17 +379,11 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
 #pragma unroll
       for (int i = 0; i < PF; ++i) {
         wait_page<(PF - 1) * kLoadsPerPage, D>(r[i]);
-        const int idx = base + k + i;
-        const int page = first + NW * idx;
+        const int page = first + NW * (base + k + i);
         const int limit = (k + i < here) ? seq_len : 0;
         process_page<D>(st, r[i], qb, tile, n, g, page * 16 + 4 * g, limit, a.scale_log2);
         const int64_t pn = phys(min(k + i + PF, here - 1)) * a.c_sb;
         load_page<D>(r[i], kc + pn, vc + pn, off);
-        // End of a full split that is not the group's last: every wave is here.
-        if (gps > 1 && k + i < here && (idx + 1) % ppw == 0 && j_cur < j1 - 1 && (j_cur + 1) * bps <= n_blocks) {
-          finish_split(j_cur);
-          ++j_cur;
-        }
       }
     }
     // Drain: the loads issued for pages past the end must land before their
@@ -370,139 +391,13 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
 #pragma unroll
     for (int i = 0; i < PF; ++i) wait_page<0, D>(r[i]);
   }
-  // The split holding the wave's last pages, then the group's splits that the
-  // row does not reach (zero output, -inf LSE).
-  for (; j_cur < j1; ++j_cur) finish_split(j_cur);
-}
 
-// One split of one (sequence, KV head) on a single wave, for plans with many
-// short splits. The wave keeps the NW = 4 states that the waves of a
-// decode_work_group would keep (state s takes the split's pages start + s,
-// start + s + 4, ...), computes each page with the same process_page, and
-// merges the four states in registers with merge_states' arithmetic (max in
-// state order, then fma chains in state order), so the bits equal those of
-// decode_work_group for the same split. No LDS merge records and no
-// barriers: the wave needs no other wave. `tile` is the wave's private K
-// transpose tile (kTileBytes<D> bytes).
-template <int D, int PF>
-__device__ __forceinline__ void decode_split_wave(const DecodeArgs& a, const int item, unsigned char* tile) {
-  constexpr int KC = D / 32;
-  constexpr int VD = D / 16;
-  constexpr int NS = 4;  // the states of a 4-wave work-group
-  static_assert(PF == 2 || PF == 4, "pages in flight per wave");
-
-  const int G = a.num_heads / a.num_kv_heads;
-  const int split = item % a.num_splits;
-  const int bk = item / a.num_splits;
-  const int kvh = bk % a.num_kv_heads;
-  const int b = bk / a.num_kv_heads;
-
-  const int lane = lane_id();
-  const int n = lane & 15;
-  const int g = lane >> 4;
-
-  const int seq_len = uniform(a.seq_lens[b]);
-  int n_blocks = seq_len > 0 ? (seq_len + 15) / 16 : 0;
-  n_blocks = min(n_blocks, a.max_blocks);
-  const int start = split * a.blocks_per_split;
-  // The last split of the row runs to the row's last page.
-  const int end = (split == a.num_splits - 1) ? n_blocks : min(start + a.blocks_per_split, n_blocks);
-  const int cnt = max(end - start, 0);
-
-  uint4 qb[KC];
-  {
-    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_sb +
-                           (int64_t)(kvh * G + n) * a.q_sh;
-#pragma unroll
-    for (int c = 0; c < KC; ++c) qb[c] = (n < G) ? ld16(qrow + 8 * (4 * c + g)) : make_uint4(0, 0, 0, 0);
-  }
-
-  WaveState<D> st[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    st[s].m = kNegInf;
-    st[s].l = 0.f;
-#pragma unroll
-    for (int c = 0; c < VD; ++c) st[s].acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  }
-
-  uint32_t off[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) off[j] = (uint32_t)((4 * g + j) * a.c_st + VD * n);
-  const uint16_t* kc = reinterpret_cast<const uint16_t*>(a.k_cache) + (int64_t)kvh * a.c_sh;
-  const uint16_t* vc = reinterpret_cast<const uint16_t*>(a.v_cache) + (int64_t)kvh * a.c_sh;
-  const int32_t* bt = a.block_tables + (int64_t)b * a.bt_stride;
-
-  // Pages are taken four at a time (one per state), PF in flight; loads are
-  // issued for clamped page indices, and pages past the split's end are
-  // skipped (a fully masked page would leave its state bit-identical anyway).
-  for (int base = 0; base < cnt; base += 64) {
-    const int here = min(64, cnt - base);
-    const int ent = bt[min(start + base + lane, a.max_blocks - 1)];
-    const int slot_ent = min(max(ent, 0), a.num_pages - 1);
-    auto phys = [&](int k) -> int64_t { return (int64_t)__builtin_amdgcn_readlane(slot_ent, k); };
-    PageRegs<D> r[PF];
-#pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      const int64_t p = phys(min(i, here - 1)) * a.c_sb;
-      load_page<D>(r[i], kc + p, vc + p, off);
-    }
-    const int padded = (here + NS - 1) / NS * NS;
-    for (int k = 0; k < padded; k += NS) {
-#pragma unroll
-      for (int i = 0; i < NS; ++i) {
-        wait_page<(PF - 1) * kLoadsPerPage, D>(r[i % PF]);
-        const int page = start + base + k + i;
-        if (k + i < here)
-          process_page<D>(st[i], r[i % PF], qb, tile, n, g, page * 16 + 4 * g, seq_len, a.scale_log2);
-        const int64_t pn = phys(min(k + i + PF, here - 1)) * a.c_sb;
-        load_page<D>(r[i % PF], kc + pn, vc + pn, off);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < PF; ++i) wait_page<0, D>(r[i]);
-  }
-
-  // merge_states' arithmetic, per lane: head n, dims (D/16)·(4g+i) + c.
-  float lt[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) lt[s] = sum_across_groups(st[s].l);
-  float M = kNegInf;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) M = fmaxf(M, st[s].m);
-  float L = 0.f;
-  f32x4_t A[VD];
-#pragma unroll
-  for (int c = 0; c < VD; ++c) A[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  if (M != kNegInf) {
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const float wgt = fast_exp2(st[s].m - M);
-      L = __builtin_fmaf(lt[s], wgt, L);
-#pragma unroll
-      for (int c = 0; c < VD; ++c)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) A[c][i] = __builtin_fmaf(st[s].acc[c][i], wgt, A[c][i]);
-    }
-  }
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  if (n >= G) return;
-  const int head = kvh * G + n;
-  const int64_t prow = ((int64_t)b * a.num_heads + head) * a.num_splits + split;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float o[VD];
-#pragma unroll
-    for (int c = 0; c < VD; ++c) o[c] = L == 0.f ? 0.f : A[c][i] * inv;
-    float* dst = a.part_out + prow * D + VD * (4 * g + i);
-    if constexpr (VD == 8) {
-      *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
-      *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
-    } else {
-      *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
-    }
-  }
-  if (g == 0) a.part_lse[prow] = (L > 0.f) ? M + __log2f(L) : kNegInf;
+  // Merge records (m[16], l[16], acc[G][D] per wave) follow the NW K tiles.
+  const int wstride = 32 + G * D;
+  float* merge = smem + NW * kTileBytes<D> / 4;
+  save_state<D>(merge + w * wstride, st, sum_across_groups(st.l), G, n, g);
+  __syncthreads();
+  merge_states<D, NW>(a, merge, wstride, G, row, kvh, threadIdx.x, NW * 64);
 }
 
 }  // namespace bvllm

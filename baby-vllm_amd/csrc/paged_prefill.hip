@@ -629,7 +629,6 @@ static DecodeArgs single_query_view(const PrefillArgs& p) {
   a.num_splits = 1; a.blocks_per_split = p.max_blocks;
   a.batch = p.num_seqs; a.num_heads = p.num_heads; a.num_kv_heads = p.num_kv_heads; a.head_dim = p.head_dim;
   a.waves = kDecodeWaves;
-  a.splits_per_wg = 1;
   a.query_start_loc = p.query_start_loc;
   a.context_lens = p.context_lens;
   return a;
@@ -694,12 +693,11 @@ static hipError_t launch_prefill(const PrefillArgs& a, const PrefillGrid& p, int
 // two work-groups per CU, a work-group takes several blocks of one (sequence,
 // KV head), which read the same tiles: the fewest per work-group that make
 // the grid one round (64 x 128: 4 blocks per work-group, 512 work-groups).
-// BVLLM_PREFILL_BLOCKS_PER_WG overrides the choice when the table width allows
-// it (read per launch: tests vary it).
+// The tuning switch kTunePrefillBlocksPerWg overrides the choice when the
+// table width allows it.
 static int prefill_blocks_per_wg(const PrefillArgs& a, const PrefillGrid& p1) {
   if (a.max_blocks > 8) return 1;
-  const char* env = getenv("BVLLM_PREFILL_BLOCKS_PER_WG");
-  const int forced = env ? atoi(env) : 0;
+  const int forced = tuning(kTunePrefillBlocksPerWg);
   if (forced > 0) return forced;
   if (p1.dense_qb <= 1) return 1;
   const int64_t slots = 2 * (int64_t)device_cus();

@@ -37,7 +37,7 @@ extern "C" {
 #endif
 
 /* ABI version of this header; bumped on any signature change. */
-#define BVLLM_ABI_VERSION 5
+#define BVLLM_ABI_VERSION 6
 
 #if defined(__GNUC__)
 #define BVLLM_API __attribute__((visibility("default")))
@@ -75,8 +75,10 @@ BVLLM_API int bvllm_rope_kv_append(void* q, int64_t q_stride_t, int64_t q_stride
 
 /*
  * Bytes of device scratch bvllm_paged_decode needs for one launch (0 = none):
- * fp32 partial outputs [B, H, S, D] and log-sum-exps [B, H, S] of every split,
- * the reference's part_out / part_lse (babyvllm/kernels/paged_attn.py:317-318).
+ * fp32 partial outputs [B, H, P, D] and log-sum-exps [B, H, P], the
+ * reference's part_out / part_lse (babyvllm/kernels/paged_attn.py:317-318),
+ * where P is the number of splits, or of groups of 4 consecutive splits when
+ * the launch folds each group before writing it (plans with many splits).
  */
 BVLLM_API int64_t bvllm_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                                                int32_t head_dim, int32_t num_splits,
@@ -94,8 +96,11 @@ BVLLM_API int64_t bvllm_decode_workspace_bytes(int32_t batch, int32_t num_heads,
  * (decode_split_plan, babyvllm/kernels/decode_split.py:48-79): split s covers
  * pages [s·bps, (s+1)·bps), the last split runs to the row's last page.
  * `workspace` must hold bvllm_decode_workspace_bytes() bytes when that is > 0.
- * `waves` is the number of 64-lane waves per work-group: 0 (the library's
- * choice), 4 or 8; launches whose bits are compared must use the same value.
+ * `waves` is the number of 64-lane waves per single-pass work-group: 0 (the
+ * library's choice) or 4.
+ * Bits: a row that fits in one split gives the same output from the single
+ * pass and from any split plan, and a plan sized for a longer context (a graph
+ * bucket) gives the same output as one sized for the live lengths.
  */
 BVLLM_API int bvllm_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                        const void* k_cache, const void* v_cache,
@@ -167,6 +172,18 @@ BVLLM_API int bvllm_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_s
                         int32_t single_query_seqs,
                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                         int32_t block_size, void* stream);
+
+/*
+ * Tuning switch for experiments and tests (no counterpart in the reference):
+ * sets process-wide knob `knob` to `value` (0 = the library's default) and
+ * returns the previous value, or -1 for an unknown knob. Knobs: 0 decode split
+ * mode (1 one wave per split, 2 one wave per group of 4 splits), 1 prefill
+ * column blocks per work-group (tables of at most 8 pages), 2 decode wave
+ * order (1 split units fastest), 3 decode single pass on streaming waves (1),
+ * 4 decode page loads of the streaming waves without the nontemporal hint
+ * (1). No knob changes any result bit.
+ */
+BVLLM_API int bvllm_set_tuning(int32_t knob, int32_t value);
 
 /*
  * Greedy sampling: out[r] = argmax(logits[r, :]) for rows r < rows. Replaces

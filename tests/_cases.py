@@ -7,6 +7,8 @@ Builders follow the reference's fixtures: ``make_decode_inputs`` is
 
 from __future__ import annotations
 
+from contextlib import contextmanager
+
 import torch
 
 from babyvllm.worker.context import AttentionMetadata
@@ -113,3 +115,14 @@ def md_to_cpu(md):
         seq_lens_cpu=md.seq_lens_cpu, context_lens_cpu=md.context_lens_cpu,
         max_query_len=md.max_query_len, max_seq_len=md.max_seq_len,
     )
+
+
+@contextmanager
+def tuned(knob: int, value: int):
+    """Sets a library tuning knob (bvllm_set_tuning) for the block, then restores it."""
+    from babyvllm.kernels import _lib
+    prev = _lib.set_tuning(knob, value)
+    try:
+        yield
+    finally:
+        _lib.set_tuning(knob, prev)

@@ -38,8 +38,9 @@ pytestmark = [
 ]
 
 # bf16 activations through 2 layers and bf16 logits (ulp 2^-7 .. 2^-5 at the
-# logits' magnitude, max |logit| about 6) against fp32: stated tolerances on
-# each position's logits row (max-abs over the 152,064 logits, and mean-abs).
+# logits' magnitude; logits ~ N(0, 1.2^2), max |logit| about 6) against fp32:
+# stated tolerances on each position's logits row (max-abs over the 152,064
+# logits, and mean-abs; measured 0.10 and 0.017).
 LOGIT_MAX_TOL = 0.15
 LOGIT_MEAN_TOL = 0.025
 # Near-tie threshold for the graph / eager / caching comparison.

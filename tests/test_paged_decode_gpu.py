@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from oracle import attention as oa
-from tests._cases import BLOCK_SIZE, assert_attn_close, cdiv, make_decode_inputs, scale_keys_by_position
+from tests._cases import BLOCK_SIZE, assert_attn_close, cdiv, make_decode_inputs, scale_keys_by_position, tuned
 
 pytestmark = [
     pytest.mark.gpu,
@@ -206,58 +206,57 @@ def test_reduce_bits_do_not_depend_on_the_split_count(n, monkeypatch):
     assert_attn_close(graph, _oracle(q, kv_cache, bt, [n], scale))
 
 
-@pytest.mark.parametrize("lens", [[600, 37, 0], [2047, 1, 64], [130, 129, 128, 127]])
-def test_splits_per_work_group_do_not_change_bits(lens, monkeypatch):
-    """One work-group may compute several consecutive splits (its page loads
-    run on across split boundaries); every split's state, and so the output,
-    stays bit-identical. Rows ending inside a group make padding pages open a
-    split's state, which must leave it empty (not NaN)."""
-    from babyvllm.kernels.decode_split import DECODE_PARTITION_ENV
+def _modes(q, kv_cache, bt, seq_lens, scale, bucket, partition):
+    """Outputs of every launch choice that must give the same bits: split mode
+    (one wave per split, one wave per group of 4 splits), wave order,
+    nontemporal page loads, single pass on streaming waves."""
+    from babyvllm.kernels import _lib
 
-    monkeypatch.delenv(DECODE_PARTITION_ENV, raising=False)
-    monkeypatch.setenv("BVLLM_DECODE_SPLIT_WAVES", "0")  # the work-group path
-    scale = HEAD_DIM ** -0.5
-    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, width=300, seed=len(lens))
-    outs = []
-    for gps in (1, 2, 3, 4, 8):
-        monkeypatch.setenv("BVLLM_DECODE_SPLITS_PER_WG", str(gps))
-        outs.append(_kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=4096, partition_blocks=4))
-    for out in outs[1:]:
-        assert torch.equal(out, outs[0])
-    assert not torch.isnan(outs[0]).any()
-    assert_attn_close(outs[0], _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
-
-
-@pytest.mark.parametrize("partition", [1, 2, 3, 4, 7, 8, 16])
-@pytest.mark.parametrize("lens", [[600, 37, 0, 1], [2047, 16, 64, 300], [5000, 129]])
-def test_split_per_wave_matches_work_group_bits(partition, lens, monkeypatch):
-    """Short splits run one per wave, which keeps the four per-wave states of a
-    work-group in registers and merges them with the work-group's arithmetic:
-    the bits equal those of the work-group path for every split plan, also for
-    a row longer than the bucket (its last split runs to the row's end)."""
-    from babyvllm.kernels.decode_split import DECODE_PARTITION_ENV
-
-    monkeypatch.delenv(DECODE_PARTITION_ENV, raising=False)
-    scale = HEAD_DIM ** -0.5
-    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, width=320, seed=partition + len(lens))
     outs = {}
-    for mode in ("0", "1"):
-        monkeypatch.setenv("BVLLM_DECODE_SPLIT_WAVES", mode)
-        outs[mode] = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=4096, partition_blocks=partition)
-    assert torch.equal(outs["0"], outs["1"])
-    assert not torch.isnan(outs["1"]).any()
-    assert_attn_close(outs["1"], _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
+    choices = [("auto", None, 0), ("per_split", _lib.TUNE_DECODE_SPLIT_MODE, 1),
+               ("per_group", _lib.TUNE_DECODE_SPLIT_MODE, 2),
+               ("order1", _lib.TUNE_DECODE_ORDER, 1), ("cached", _lib.TUNE_DECODE_CACHED, 1),
+               ("stream_single", _lib.TUNE_DECODE_SINGLE_PASS_STREAM, 1)]
+    for name, knob, value in choices:
+        if knob is None:
+            outs[name] = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=bucket, partition_blocks=partition)
+            continue
+        with tuned(knob, value):
+            outs[name] = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=bucket,
+                                   partition_blocks=partition)
+    return outs
 
 
-@pytest.mark.parametrize("hkv,group,d", [(2, 7, 64), (1, 16, 128), (8, 4, 128)])
-def test_split_per_wave_other_head_configs(hkv, group, d, monkeypatch):
-    monkeypatch.setenv("BVLLM_DECODE_SPLIT_WAVES", "1")
+@pytest.mark.parametrize("partition", [None, 0, 1, 2, 3, 4, 7, 8, 16])
+@pytest.mark.parametrize("lens", [[600, 37, 0, 1], [2047, 16, 64, 300], [5000, 129], [130, 129, 128, 127]])
+def test_launch_choices_do_not_change_bits(partition, lens, monkeypatch):
+    """Every launch choice of one plan gives identical bits: one wave per
+    split (groups of 4 splits folded in the reduce) or per group (folded in
+    the wave), either wave order, with or without the nontemporal hint, and the single pass on work-groups or streaming waves.
+    Rows longer than the bucket and rows ending inside a group are covered."""
+    from babyvllm.kernels.decode_split import DECODE_PARTITION_ENV
+
+    monkeypatch.delenv(DECODE_PARTITION_ENV, raising=False)
+    scale = HEAD_DIM ** -0.5
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, width=330, seed=len(lens) + (partition or 0))
+    outs = _modes(q, kv_cache, bt, seq_lens, scale, 4096, partition)
+    for name, out in outs.items():
+        assert torch.equal(out, outs["auto"]), name
+    assert not torch.isnan(outs["auto"]).any()
+    assert_attn_close(outs["auto"], _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
+
+
+@pytest.mark.parametrize("hkv,group,d", [(2, 7, 64), (1, 16, 128), (8, 4, 128), (4, 1, 64)])
+def test_launch_choices_other_head_configs(hkv, group, d):
     lens = [700, 33, 0, 1500]
     q, kv_cache, bt, seq_lens = make_decode_inputs(lens, width=128, seed=hkv * 10 + group, hkv=hkv, group=group,
                                                    d=d)
     scale = d ** -0.5
-    out = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=2048, partition_blocks=4)
-    assert_attn_close(out, _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
+    for partition in (4, 0):
+        outs = _modes(q, kv_cache, bt, seq_lens, scale, 2048, partition)
+        for name, out in outs.items():
+            assert torch.equal(out, outs["auto"]), name
+        assert_attn_close(outs["auto"], _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
 
 
 @pytest.mark.parametrize("partition", [0, 1, 4])

@@ -9,7 +9,9 @@ import pytest
 import torch
 
 from oracle import attention as oa
-from tests._cases import assert_attn_close, build_prefill_case, md_to_cpu, scale_keys_by_position
+from tests._cases import assert_attn_close, build_prefill_case, md_to_cpu, scale_keys_by_position, tuned
+
+_BPW = 1  # tuning knob: prefill column blocks per work-group (bvllm_set_tuning)
 
 pytestmark = [
     pytest.mark.gpu,
@@ -204,7 +206,7 @@ def test_scores_rising_along_the_sequence(growth, hkv, group, d):
 
 @pytest.mark.parametrize("bpw", [2, 3, 4, 7, 64])
 @pytest.mark.parametrize("hkv,group,d", [(4, 7, 128), (8, 3, 64), (1, 16, 128)])
-def test_blocks_per_work_group_do_not_change_bits(bpw, hkv, group, d, monkeypatch):
+def test_blocks_per_work_group_do_not_change_bits(bpw, hkv, group, d):
     """When every sequence fits two 64-key tiles (table width ≤ 8 pages), a
     work-group may compute several column blocks of one (sequence, KV head)
     over tiles staged once; any number of blocks per work-group gives the
@@ -214,15 +216,15 @@ def test_blocks_per_work_group_do_not_change_bits(bpw, hkv, group, d, monkeypatc
                                                     (127, 1)]
     q, kv_cache, md = build_prefill_case(specs, hkv, group, d, seed=bpw)
     assert md.block_tables.shape[1] <= 8
-    monkeypatch.setenv("BVLLM_PREFILL_BLOCKS_PER_WG", "1")
-    one = _kernel()(q, kv_cache, md, d ** -0.5)
-    monkeypatch.setenv("BVLLM_PREFILL_BLOCKS_PER_WG", str(bpw))
-    many = _kernel()(q, kv_cache, md, d ** -0.5)
+    with tuned(_BPW, 1):
+        one = _kernel()(q, kv_cache, md, d ** -0.5)
+    with tuned(_BPW, bpw):
+        many = _kernel()(q, kv_cache, md, d ** -0.5)
     assert torch.equal(one, many)
     assert_attn_close(many, _oracle(q, kv_cache, md, group))
 
 
-def test_scores_rising_with_blocks_per_work_group(monkeypatch):
+def test_scores_rising_with_blocks_per_work_group():
     """The rescale path on the multi-block kernel: every sequence within two
     64-key tiles, a grid large enough for several blocks per work-group, key
     norms growing with position; same bits as one block per work-group."""
@@ -231,8 +233,8 @@ def test_scores_rising_with_blocks_per_work_group(monkeypatch):
     assert md.block_tables.shape[1] <= 8
     scale_keys_by_position(kv_cache, md.block_tables, md.seq_lens_cpu, lambda p: 1.0 + p / 12.0)
     many = _kernel()(q, kv_cache, md, 128 ** -0.5)
-    monkeypatch.setenv("BVLLM_PREFILL_BLOCKS_PER_WG", "1")
-    one = _kernel()(q, kv_cache, md, 128 ** -0.5)
+    with tuned(_BPW, 1):
+        one = _kernel()(q, kv_cache, md, 128 ** -0.5)
     assert torch.equal(one, many)
     assert_attn_close(many, _oracle(q, kv_cache, md, 7))
 
@@ -263,7 +265,7 @@ def test_random_varlen_batches(seed):
 
 
 @pytest.mark.parametrize("seed", range(8))
-def test_random_short_batches_against_one_block_per_work_group(seed, monkeypatch):
+def test_random_short_batches_against_one_block_per_work_group(seed):
     """Seeded random steps of 24-80 sequences that all fit two 64-key tiles,
     where the host gives a work-group several column blocks whenever the grid
     allows it: within tolerance of the oracle and bit-equal to one block per
@@ -277,10 +279,9 @@ def test_random_short_batches_against_one_block_per_work_group(seed, monkeypatch
         specs.append((ctx, q_len))
     q, kv_cache, md = build_prefill_case(specs, hkv, group, d, seed=seed)
     assert md.block_tables.shape[1] <= 8
-    monkeypatch.delenv("BVLLM_PREFILL_BLOCKS_PER_WG", raising=False)
     auto = _kernel()(q, kv_cache, md, d ** -0.5)
-    monkeypatch.setenv("BVLLM_PREFILL_BLOCKS_PER_WG", "1")
-    one = _kernel()(q, kv_cache, md, d ** -0.5)
+    with tuned(_BPW, 1):
+        one = _kernel()(q, kv_cache, md, d ** -0.5)
     assert torch.equal(auto, one)
     assert_attn_close(auto, _oracle(q, kv_cache, md, group))
 
