@@ -16,11 +16,16 @@ Infinity Cache), exactly the reference's method (benchmarks/bench_decode_attn.py
   cpu_baseline = the oracle's restatement of the reference's torch decode path
              (gather + SDPA, fp32) timed on this host on the same workload
 
-Secondary lines (same method): decode B8/ctx1920, B1/ctx32768, B64/ctx2048 (the
-reference's published H100 point), RoPE + KV append (decode 64 tokens, prefill
-8192 tokens), the four varlen prefill configurations in TFLOP/s, and the decode
-step's other kernels (greedy argmax over 64 x 152,064 logits, residual add +
-RMSNorm and SiLU*mul at 64 and 8192 rows) in GB/s.
+Secondary lines (same method), each with its binding roof and the oracle's
+restatement of the reference's torch CPU path timed on this host beside it:
+BASELINE config 1 (the 0.5B-shape single-layer step: RoPE + append + decode),
+decode B8/ctx1920, B1/ctx32768, B64/ctx2048 (the reference's published H100
+point), RoPE + KV append (decode 64 tokens, prefill 8192 tokens), the four
+varlen prefill configurations (TFLOP/s; fraction of the binding roof, MFMA or
+HBM), the decode step's other kernels (greedy argmax over 64 x 152,064 logits,
+residual add + RMSNorm and SiLU*mul at 64 and 8192 rows) in GB/s, and the
+end-to-end generate of config 5. The host CPU (lscpu model, sockets, cores,
+threads) is recorded once in `cpu_host`.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
                        [--only NAME] [--calib-copy]
@@ -32,6 +37,7 @@ import argparse
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -130,6 +136,7 @@ def bench_decode(batch, ctx, warmup, iters, layers=LAYERS):
         "frac_of_hbm_peak": kv_bytes / (per_launch_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
         "kv_bytes_per_layer": kv_bytes,
         "step_ms": ms,
+        "roofline": hbm_roof(kv_bytes, per_launch_us * 1e-6),
     }
 
 
@@ -177,7 +184,7 @@ def bench_append(tokens_per_seq, seqs, warmup, iters, layers=LAYERS):
     torch.cuda.empty_cache()
     return {"tokens": T, "us_per_layer": per_us, "gb_s": nbytes / (per_us * 1e-6) / 1e9,
             "frac_of_hbm_peak": nbytes / (per_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-            "algorithmic_bytes": nbytes}
+            "algorithmic_bytes": nbytes, "roofline": hbm_roof(nbytes, per_us * 1e-6)}
 
 
 PREFILL_SHAPES = {
@@ -190,6 +197,32 @@ PREFILL_SHAPES = {
 
 def prefill_flops(specs):
     return 512 * H * sum(sum(c + i + 1 for i in range(n)) for c, n in specs)
+
+
+def prefill_bytes(specs):
+    """Algorithmic HBM bytes: q read and output written once, each sequence's K/V read once per KV head."""
+    tokens = sum(n for _, n in specs)
+    return 2 * tokens * H * D * 2 + sum(c + n for c, n in specs) * HKV * D * 2 * 2
+
+
+def hbm_roof(nbytes, seconds):
+    ach = nbytes / seconds / 1e9
+    return {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes}
+
+
+def binding_roof(flops, nbytes, seconds):
+    """The roof that binds at peak (the longer of flops / bf16 MFMA peak and bytes / HBM peak)."""
+    t_mfma = flops / (BF16_PEAK_TFLOPS * 1e12)
+    t_hbm = nbytes / (HBM_PEAK_GBS * 1e9)
+    if t_mfma >= t_hbm:
+        ach = flops / seconds / 1e12
+        out = {"bound": "mfma", "achieved": round(ach, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+               "frac": round(t_mfma / seconds, 4)}
+    else:
+        out = hbm_roof(nbytes, seconds)
+    out.update({"roof_us": round(max(t_mfma, t_hbm) * 1e6, 2), "flop": flops, "algorithmic_bytes": nbytes})
+    return out
 
 
 def bench_prefill(name, warmup, iters, layers=LAYERS):
@@ -232,8 +265,67 @@ def bench_prefill(name, warmup, iters, layers=LAYERS):
     flops = prefill_flops(specs)
     del caches, mds, q
     torch.cuda.empty_cache()
-    return {"us_per_layer": per_us, "tflop_s": flops / (per_us * 1e-6) / 1e12,
-            "frac_of_bf16_peak": flops / (per_us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, "flop": flops}
+    return {"us_per_layer": per_us, "tflop_s": flops / (per_us * 1e-6) / 1e12, "flop": flops,
+            "roofline": binding_roof(flops, prefill_bytes(specs), per_us * 1e-6)}
+
+
+# the 0.5B-shape single-layer decode step.
+C1_H, C1_HKV, C1_D, C1_B, C1_POOL, C1_WIDTH, C1_BUCKET = 14, 2, 64, 8, 512, 32, 512
+
+
+def config1_inputs(seed, device):
+    """Lengths U[100, 512], a 512-block pool whose rows are a seeded permutation
+    (width 32), q/k/v ~ N(0, 1); the step's token sits at position seq_len - 1."""
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(100, 513, (C1_B,), generator=g)
+    cache = torch.randn(2, C1_POOL, BS, C1_HKV, C1_D, generator=g)
+    bt = torch.randperm(C1_POOL, generator=g)[: C1_B * C1_WIDTH].view(C1_B, C1_WIDTH).int()
+    qkv = torch.randn(C1_B, (C1_H + 2 * C1_HKV) * C1_D, generator=g)
+    pos = lens - 1
+    slots = bt[torch.arange(C1_B), pos // BS].long() * BS + pos % BS
+    dt = torch.bfloat16 if device != "cpu" else torch.float32
+    return (lens.to(device), cache.to(device, dt), bt.to(device), qkv.to(device, dt), pos.to(device),
+            slots.to(device))
+
+
+def config1_bytes(lens):
+    """Append 5,128 B per token (q, k, v, cos, sin, slot read; q, k, cache rows written) + KV read."""
+    return C1_B * 5128 + int(lens.sum()) * C1_HKV * C1_D * 2 * 2
+
+
+def bench_config1(warmup, iters, layers=24):
+    """One 'step' = the config-1 step for each of the 0.5B model's 24 layers, each
+    layer on its own 512-block pool: RoPE (theta 1e6) + append through
+    slot_mapping, then paged decode with max_seq_len = 512."""
+    from babyvllm.kernels.paged_attn import paged_decode_attention
+    from babyvllm.kernels.rope import fused_rope_and_cache
+    from babyvllm.layers.rotary import RotaryEmbedding
+
+    per_layer = [config1_inputs(100 + i, "cuda") for i in range(layers)]
+    lens, _, _, _, pos, _ = per_layer[0]
+    seq_lens = lens.int()
+    rope = RotaryEmbedding(C1_D, 4096, base=1e6).cuda()
+    views = []
+    for _, cache, bt, qkv, _, slots in per_layer:
+        q = qkv[:, : C1_H * C1_D].view(C1_B, C1_H, C1_D)
+        k = qkv[:, C1_H * C1_D:(C1_H + C1_HKV) * C1_D].view(C1_B, C1_HKV, C1_D)
+        v = qkv[:, (C1_H + C1_HKV) * C1_D:].view(C1_B, C1_HKV, C1_D)
+        views.append((q, k, v, cache, bt, slots))
+
+    def fwd():
+        cos, sin = rope(pos, torch.bfloat16)
+        for q, k, v, cache, bt, slots in views:
+            fused_rope_and_cache(q, k, v, cos, sin, cache, slots)
+            paged_decode_attention(q, cache, bt, seq_lens, C1_D ** -0.5, max_seq_len=C1_BUCKET)
+
+    ms, _ = time_graph(fwd, warmup, iters)
+    per_us = ms * 1e3 / layers
+    nbytes = config1_bytes(lens.cpu())
+    del per_layer, views
+    torch.cuda.empty_cache()
+    return {"us_per_layer": per_us, "gb_s": nbytes / (per_us * 1e-6) / 1e9, "algorithmic_bytes": nbytes,
+            "roofline": hbm_roof(nbytes, per_us * 1e-6),
+            "note": "latency-bound: 1.3 MB per step, 0.16 us at the HBM roof"}
 
 
 def bench_step_kernels(warmup, iters):
@@ -250,7 +342,8 @@ def bench_step_kernels(warmup, iters):
     def line(name, per_us, nbytes, reps):
         out[name] = {"us_per_call": per_us, "gb_s": nbytes / (per_us * 1e-6) / 1e9,
                      "frac_of_hbm_peak": nbytes / (per_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-                     "algorithmic_bytes": nbytes, "calls_per_replay": reps}
+                     "algorithmic_bytes": nbytes, "calls_per_replay": reps,
+                     "roofline": hbm_roof(nbytes, per_us * 1e-6)}
 
     g = torch.Generator(device="cuda").manual_seed(11)
     reps = 16
@@ -342,35 +435,183 @@ def bench_generate(n_prompts=64, prompt_len=1920, shared_len=1536, new_tokens=64
 
 
 # ------------------------------------------------------------ CPU baseline
+#
+# The reference's torch CPU path, restated by the oracle (gather + SDPA decode,
+# per-sequence SDPA prefill loop, apply_rope + index_copy_ store), in fp32 (the
+# reference's CPU dtype), on the same shapes as the GPU lines, on this host's
+# cores. Median of at least 5 runs after one warm-up, within a time budget.
 
-def cpu_baseline(batch, ctx, budget_s=15.0):
-    """Oracle restatement of the reference's torch decode (gather + SDPA, fp32) on this host."""
+def cpu_threads():
+    """CPUs this process may use (its affinity mask, capped by OMP_NUM_THREADS when set)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_host():
+    """lscpu model, sockets, cores and threads of this host, and the threads the baseline uses."""
+    info = {"threads_used": cpu_threads(), "os_cpu_count": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        fields = {}
+        for line in out.splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                fields[k.strip()] = v.strip()
+        info.update({"model": fields.get("Model name"), "sockets": fields.get("Socket(s)"),
+                     "cores_per_socket": fields.get("Core(s) per socket"),
+                     "threads_per_core": fields.get("Thread(s) per core"), "cpus": fields.get("CPU(s)")})
+        try:
+            info["physical_cores"] = int(fields["Socket(s)"]) * int(fields["Core(s) per socket"])
+        except (KeyError, ValueError):
+            pass
+    except (OSError, subprocess.SubprocessError):
+        info["model"] = None
+    return info
+
+
+def cpu_time(fn, budget_s=10.0, min_runs=5, max_runs=50):
+    torch.set_num_threads(cpu_threads())
+    fn()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_runs or (time.perf_counter() < t_end and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def _cpu_line(value, unit, sec, runs, sample):
+    return {"value": round(value, 4), "unit": unit, "cores": cpu_threads(), "kind": "port",
+            "ms": round(sec * 1e3, 3), "runs": runs, "sample": sample}
+
+
+def cpu_decode(batch, ctx, budget_s=10.0):
+    """Oracle static_decode_attention (gather + SDPA, fp32) on one layer of the workload."""
     from oracle import attention as oa
 
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
     blocks = cdiv(ctx, BS)
     cache = torch.randn(2, batch * blocks, BS, HKV, D, generator=g)
     bt = torch.randperm(batch * blocks, generator=g).view(batch, blocks).int()
     q = torch.randn(batch, H, D, generator=g)
     lens = torch.full((batch,), ctx, dtype=torch.int32)
-    oa.static_decode_attention(q, cache, bt, lens, ctx, D ** -0.5)  # warm-up
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 50):
-        t0 = time.perf_counter()
-        oa.static_decode_attention(q, cache, bt, lens, ctx, D ** -0.5)
-        times.append(time.perf_counter() - t0)
-    sec = statistics.median(times)
+    sec, runs = cpu_time(lambda: oa.static_decode_attention(q, cache, bt, lens, ctx, D ** -0.5), budget_s)
     kv_bytes = batch * ctx * HKV * D * 2 * 2
-    return {
-        "value": kv_bytes / sec / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
-        "kind": "port",
-        "sample": (f"oracle static_decode_attention (gather + SDPA, fp32) on one layer of the "
-                   f"same workload (B{batch}, ctx {ctx}, 7B shape), median of {len(times)} runs, "
-                   f"{sec * 1e3:.1f} ms per layer"),
-    }
+    return _cpu_line(kv_bytes / sec / 1e9, "GB/s", sec, runs,
+                     f"oracle static_decode_attention (gather + SDPA, fp32), one layer of B{batch} x ctx {ctx} "
+                     f"(7B shape), median of {runs} runs; GB/s of the same bf16 KV bytes as the GPU line")
+
+
+def cpu_append(tokens_per_seq, seqs, budget_s=5.0):
+    """Oracle apply_rope + store_kvcache (index_copy_) in fp32 on the same token count."""
+    from oracle import rope as orope
+
+    T = tokens_per_seq * seqs
+    g = torch.Generator().manual_seed(T)
+    q = torch.randn(T, H, D, generator=g)
+    k = torch.randn(T, HKV, D, generator=g)
+    v = torch.randn(T, HKV, D, generator=g)
+    ct, st = orope.rope_tables(D, 4097, 1e6)
+    pos = (torch.randint(128, 4097, (T,), generator=g) if tokens_per_seq == 1
+           else torch.arange(tokens_per_seq).repeat(seqs))
+    cos, sin = ct[pos], st[pos]
+    cache = torch.zeros(2, 8192, BS, HKV, D)
+    slots = torch.randperm(8192 * BS, generator=g)[:T]
+
+    def run():
+        qr, kr = orope.apply_rope(q, k, cos, sin)
+        orope.store_kvcache(kr, v, cache, slots)
+
+    sec, runs = cpu_time(run, budget_s)
+    return _cpu_line(T * 19976 / sec / 1e9, "GB/s", sec, runs,
+                     f"oracle apply_rope + store_kvcache (fp32), {T} tokens at the 7B shape, median of {runs} "
+                     f"runs; GB/s of the same bf16 algorithmic bytes as the GPU line")
+
+
+def cpu_prefill(name, budget_s=10.0):
+    """Oracle paged_attention_torch (per-sequence SDPA loop, fp32) on the same shape."""
+    from oracle import attention as oa
+    from babyvllm.worker.context import AttentionMetadata
+
+    specs = PREFILL_SHAPES[name]
+    g = torch.Generator().manual_seed(len(specs))
+    seq_lens = [c + n for c, n in specs]
+    blocks = [cdiv(s_, BS) for s_ in seq_lens]
+    total = sum(blocks)
+    cache = torch.randn(2, total, BS, HKV, D, generator=g)
+    perm = torch.randperm(total, generator=g).tolist()
+    tables, i = [], 0
+    for nblk in blocks:
+        tables.append(perm[i:i + nblk] + [0] * (max(blocks) - nblk))
+        i += nblk
+    qsl = [0]
+    for _, n in specs:
+        qsl.append(qsl[-1] + n)
+    ctx = [c for c, _ in specs]
+    md = AttentionMetadata(torch.zeros(qsl[-1], dtype=torch.int64), torch.tensor(tables, dtype=torch.int32),
+                           torch.tensor(qsl, dtype=torch.int32), torch.tensor(seq_lens, dtype=torch.int32),
+                           torch.tensor(ctx, dtype=torch.int32), qsl, seq_lens, ctx, max(n for _, n in specs),
+                           max(seq_lens))
+    q = torch.randn(qsl[-1], H, D, generator=g)
+    sec, runs = cpu_time(lambda: oa.paged_attention_torch(q, cache, md, D ** -0.5, H // HKV), budget_s)
+    return _cpu_line(prefill_flops(specs) / sec / 1e12, "TFLOP/s", sec, runs,
+                     f"oracle paged_attention_torch (per-sequence SDPA loop, fp32), {name} at the 7B shape, "
+                     f"median of {runs} runs; TFLOP/s of the same visible-pair flops as the GPU line")
+
+
+def cpu_step_kernel(name, budget_s=2.0):
+    """The reference's torch path of a decode-step kernel (fp32) on the same shape:
+    torch.argmax over the logits (the greedy sampler), the oracle's add + RMSNorm
+    (babyvllm/layers/layernorm.py:27-37) and SiLU*mul."""
+    from oracle import decode_step as ods
+
+    hidden, inter, vocab = 3584, 18944, 152064
+    g = torch.Generator().manual_seed(11)
+    if name.startswith("argmax"):
+        x = torch.randn(64, vocab, generator=g)
+        fn, nbytes = (lambda: torch.argmax(x, dim=-1)), 64 * vocab * 2
+    elif name.startswith("add_rms_norm"):
+        rows = int(name.split("_")[3].split("x")[0])
+        x = torch.randn(rows, hidden, generator=g)
+        r = torch.randn(rows, hidden, generator=g)
+        w = torch.rand(hidden, generator=g)
+        fn, nbytes = (lambda: ods.fused_add_rms_norm(x, r, w, 1e-6)), rows * hidden * 2 * 4 + hidden * 2
+    else:
+        rows = int(name.split("_")[2].split("x")[0])
+        gu = torch.randn(rows, 2 * inter, generator=g)
+        fn, nbytes = (lambda: ods.silu_mul(gu)), rows * inter * 2 * 3
+    sec, runs = cpu_time(fn, budget_s)
+    return _cpu_line(nbytes / sec / 1e9, "GB/s", sec, runs,
+                     f"torch / oracle path of {name} in fp32, median of {runs} runs; GB/s of the same bf16 "
+                     f"algorithmic bytes as the GPU line")
+
+
+def cpu_config1(budget_s=5.0):
+    """Oracle step: apply_rope + store_kvcache + static_decode_attention (fp32), config 1."""
+    from oracle import attention as oa
+    from oracle import rope as orope
+
+    lens, cache, bt, qkv, pos, slots = config1_inputs(100, "cpu")
+    ct, st = orope.rope_tables(C1_D, 4096, 1e6)
+    q = qkv[:, : C1_H * C1_D].view(C1_B, C1_H, C1_D)
+    k = qkv[:, C1_H * C1_D:(C1_H + C1_HKV) * C1_D].view(C1_B, C1_HKV, C1_D)
+    v = qkv[:, (C1_H + C1_HKV) * C1_D:].view(C1_B, C1_HKV, C1_D)
+    seq_lens = lens.int()
+
+    def run():
+        qr, kr = orope.apply_rope(q, k, ct[pos], st[pos])
+        orope.store_kvcache(kr, v, cache, slots)
+        oa.static_decode_attention(qr, cache, bt, seq_lens, C1_BUCKET, C1_D ** -0.5)
+
+    sec, runs = cpu_time(run, budget_s)
+    return _cpu_line(config1_bytes(lens) / sec / 1e9, "GB/s", sec, runs,
+                     f"oracle apply_rope + store_kvcache + static_decode_attention (fp32), the config-1 step "
+                     f"(0.5B shape, B8, lengths U[100,512]), median of {runs} runs")
 
 
 def read_traffic():
@@ -409,7 +650,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary lines")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None,
-                    help="decode_b64 | decode_b8 | decode_b1 | append | prefill | prefill:<shape> | step | e2e")
+                    help="config1 | decode_b64 | decode_b8 | decode_b1 | append | prefill | prefill:<shape> | "
+                         "step | e2e | cpu")
     ap.add_argument("--calib-copy", action="store_true")
     args = ap.parse_args()
 
@@ -428,6 +670,16 @@ def main():
     from babyvllm.kernels import _lib
     _lib.lib()  # fail loudly now if the HIP library is missing
 
+    if args.only == "config1":
+        r = bench_config1(args.warmup, args.steps)
+        if not args.no_cpu:
+            r["cpu_baseline"] = cpu_config1()
+        print(json.dumps(r), flush=True)
+        return
+    if args.only == "cpu":
+        print(json.dumps({"host": cpu_host(), "decode_b64": cpu_decode(64, 1920),
+                          "prefill_1x(2048+4096)": cpu_prefill("1x(2048+4096)")}), flush=True)
+        return
     if args.only == "decode_b64":
         r = bench_decode(64, 1920, args.warmup, args.steps)
         print(json.dumps(r), flush=True)
@@ -466,21 +718,38 @@ def main():
     log(f"  {head['us_per_layer']:.2f} us/layer, {head['gb_s']:.0f} GB/s ({time.perf_counter() - t0:.1f} s)")
 
     secondary = {}
+    cpu_jobs = {}  # line name -> CPU baseline of the same workload, run after the GPU lines
     if not args.quick:
+        log("config 1: 0.5B-shape single-layer step ...")
+        secondary["config1_step_0.5b_b8"] = bench_config1(args.warmup, args.steps)
+        cpu_jobs["config1_step_0.5b_b8"] = lambda: cpu_config1()
         for b, c in ((8, 1920), (1, 32768), (64, 2048)):
             log(f"decode B{b} ctx{c} ...")
-            secondary[f"decode_b{b}_ctx{c}"] = bench_decode(b, c, args.warmup, args.steps)
+            key = f"decode_b{b}_ctx{c}"
+            secondary[key] = bench_decode(b, c, args.warmup, args.steps)
+            cpu_jobs[key] = (lambda b=b, c=c: cpu_decode(b, c, budget_s=3.0))
         log("append ...")
         secondary["append_decode_64tok"] = bench_append(1, 64, args.warmup, args.steps)
+        cpu_jobs["append_decode_64tok"] = lambda: cpu_append(1, 64, budget_s=2.0)
         secondary["append_prefill_8192tok"] = bench_append(128, 64, args.warmup, args.steps)
+        cpu_jobs["append_prefill_8192tok"] = lambda: cpu_append(128, 64, budget_s=3.0)
         for name in PREFILL_SHAPES:
             log(f"prefill {name} ...")
-            secondary[f"prefill_{name}"] = bench_prefill(name, args.warmup, max(5, args.steps // 5))
+            key = f"prefill_{name}"
+            secondary[key] = bench_prefill(name, args.warmup, max(5, args.steps // 5))
+            cpu_jobs[key] = (lambda name=name: cpu_prefill(name, budget_s=3.0))
         log("decode-step kernels (argmax, add + RMSNorm, SiLU*mul) ...")
-        secondary.update(bench_step_kernels(args.warmup, max(5, args.steps // 5)))
+        step_lines = bench_step_kernels(args.warmup, max(5, args.steps // 5))
+        secondary.update(step_lines)
+        for key in step_lines:
+            cpu_jobs[key] = (lambda key=key: cpu_step_kernel(key))
         log("end-to-end generate (config 5) ...")
         secondary["generate_shared_prefix_caching_on"] = bench_generate()
         secondary["generate_distinct_caching_off"] = bench_generate(shared_len=0, caching=False)
+        for key in ("generate_shared_prefix_caching_on", "generate_distinct_caching_off"):
+            secondary[key]["cpu_baseline"] = {
+                "value": None, "note": "not timed: the reference's torch path on the CPU would take minutes per "
+                                       "generated token of the 28-layer 7B model at 64 x 1920"}
         secondary["reference_h100_published"] = {
             "decode_b64_ctx2048_gb_s": 2514.9, "prefill_1x(2048+4096)_ms": 1.2615,
             "generate_b64_distinct_caching_off_tok_s": 1135.96, "generate_ttft_ms": 2902.94,
@@ -490,9 +759,14 @@ def main():
         }
 
     cpu = None
+    host = None
     if not args.no_cpu:
-        log("cpu baseline ...")
-        cpu = cpu_baseline(64, 1920)
+        host = cpu_host()
+        log(f"cpu baselines on {host.get('model')} ({host['threads_used']} threads) ...")
+        cpu = cpu_decode(64, 1920, budget_s=15.0)
+        for key, job in cpu_jobs.items():
+            log(f"  cpu {key} ...")
+            secondary[key]["cpu_baseline"] = job()
 
     kv_bytes = head["kv_bytes_per_layer"]
     ach = head["gb_s"]
@@ -525,6 +799,7 @@ def main():
             "launch_us": round(head["us_per_layer"], 3),
         },
         "cpu_baseline": cpu,
+        "cpu_host": host,
         "secondary": secondary,
     }
     print(json.dumps(line), flush=True)
