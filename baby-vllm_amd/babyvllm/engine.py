@@ -1,10 +1,19 @@
-"""The step loop: schedule, run the model, feed sampled tokens back (babyvllm/engine.py:24-174).
+"""The serving loop: schedule a step, run it on the model, feed the sampled tokens back.
 
+Public surface of the reference's LLMEngine (babyvllm/engine.py:24-174):
 ``LLMEngine(model_runner, max_num_batched_tokens, max_num_seqs,
-enable_prefix_caching)`` owns the KV-cache manager (sized by
-``model_runner.allocate_kv_cache()``) and the scheduler; ``step()`` returns one
-``RequestOutput`` per sequence that got a token or finished, ``run()`` steps
-until every request is done and returns the accumulated outputs per seq_id.
+enable_prefix_caching)`` sizes the KV-cache manager from
+``model_runner.allocate_kv_cache()`` and owns the scheduler; ``add_request``
+returns a request id; ``step()`` returns one ``RequestOutput`` for every
+request that received a token or finished in that step (a stop token is not
+reported as a new token); ``run()`` steps until every request is done and
+returns the accumulated output per request id; a step that can neither
+schedule, preempt nor finish anything is an error.
+
+Design of this build: ``step`` is three stages — ``_schedule_step`` (with the
+progress check), ``_execute`` (the model call and the scheduler update) and
+``_report`` (outputs for sampled and finished requests) — and ``run`` merges
+step outputs with ``RequestOutput.merge``.
 """
 
 from __future__ import annotations
@@ -12,7 +21,7 @@ from __future__ import annotations
 from dataclasses import dataclass, field
 
 from babyvllm.kv_cache_manager import KVCacheManager
-from babyvllm.scheduler import Scheduler
+from babyvllm.scheduler import Scheduler, SchedulerOutput
 from babyvllm.sequence import SamplingParams, Sequence, SequenceFinishReason
 
 
@@ -27,6 +36,11 @@ class RequestOutput:
     def finished(self) -> bool:
         return self.finish_reason is not None
 
+    def merge(self, later: "RequestOutput") -> None:
+        self.new_token_ids.extend(later.new_token_ids)
+        if later.finished:
+            self.finish_reason = later.finish_reason
+
 
 class LLMEngine:
     def __init__(self, model_runner, max_num_batched_tokens: int = 8, max_num_seqs: int = 4,
@@ -38,6 +52,8 @@ class LLMEngine:
         self.scheduler = Scheduler(self.kv_cache_manager, max_num_batched_tokens=max_num_batched_tokens,
                                    max_num_seqs=max_num_seqs)
         self.sequences: dict[int, Sequence] = {}
+
+    # --------------------------------------------------------- requests
 
     def add_request(self, token_ids: list[int], sampling_params: SamplingParams | None = None) -> int:
         seq = Sequence(token_ids, sampling_params)
@@ -53,46 +69,53 @@ class LLMEngine:
     def has_unfinished_requests(self) -> bool:
         return self.scheduler.has_unfinished()
 
-    def step(self) -> list[RequestOutput]:
-        outputs: list[RequestOutput] = []
-        reported: set[int] = set()
-        if self.has_unfinished_requests():
-            sched = self.scheduler.schedule()
-            if not (sched.scheduled_sequences or sched.preempted_seqs or self.scheduler.finished_seqs):
-                raise RuntimeError("Engine stalled: unfinished requests exist, but scheduler scheduled no "
-                                   "work, preempted nothing, and no sequences finished.")
-            if sched.scheduled_sequences:
-                sampled = self.model_runner.execute_model(sched)
-                if not isinstance(sampled, dict):
-                    raise RuntimeError("ModelRunner returned incorrect type")
-                self.scheduler.update_from_output(sched, sampled)
-                for seq in sched.scheduled_sequences:
-                    if seq.seq_id in sampled:
-                        tok = sampled[seq.seq_id]
-                        new = [] if tok in seq.sampling_params.stop_tokens else [tok]
-                        outputs.append(RequestOutput(seq.seq_id, new, seq.finish_reason))
-                        reported.add(seq.seq_id)
+    # ------------------------------------------------------------- steps
+
+    def _schedule_step(self) -> SchedulerOutput:
+        out = self.scheduler.schedule()
+        if not (out.scheduled_sequences or out.preempted_seqs or self.scheduler.finished_seqs):
+            raise RuntimeError(
+                f"no progress: {len(self.scheduler.waiting)} waiting and {len(self.scheduler.running)} running "
+                f"requests, but the step scheduled, preempted and finished nothing")
+        return out
+
+    def _execute(self, out: SchedulerOutput) -> dict[int, int]:
+        sampled = self.model_runner.execute_model(out)
+        if not isinstance(sampled, dict):
+            raise RuntimeError(f"the model runner returned {type(sampled).__name__}, expected {{seq_id: token}}")
+        self.scheduler.update_from_output(out, sampled)
+        return sampled
+
+    def _report(self, out: SchedulerOutput | None, sampled: dict[int, int]) -> list[RequestOutput]:
+        outputs: dict[int, RequestOutput] = {}
+        if out is not None:
+            for seq in out.scheduled_sequences:
+                if seq.seq_id in sampled:
+                    tok = sampled[seq.seq_id]
+                    emitted = [] if tok in seq.sampling_params.stop_tokens else [tok]
+                    outputs[seq.seq_id] = RequestOutput(seq.seq_id, emitted, seq.finish_reason)
         for seq in self.scheduler.pop_finished():
-            if seq.seq_id not in reported:
-                outputs.append(RequestOutput(seq.seq_id, [], seq.finish_reason))
+            outputs.setdefault(seq.seq_id, RequestOutput(seq.seq_id, [], seq.finish_reason))
             self.sequences.pop(seq.seq_id, None)
-        return outputs
+        return list(outputs.values())
+
+    def step(self) -> list[RequestOutput]:
+        out, sampled = None, {}
+        if self.has_unfinished_requests():
+            out = self._schedule_step()
+            if out.scheduled_sequences:
+                sampled = self._execute(out)
+        return self._report(out, sampled)
 
     def run(self, max_steps: int = 100_000) -> dict[int, RequestOutput]:
-        final: dict[int, RequestOutput] = {}
-        steps = 0
-        # Also drain sequences that finished when added (prompt too long), so
-        # every request gets an output.
-        while self.has_unfinished_requests() or self.scheduler.finished_seqs:
-            for out in self.step():
-                acc = final.setdefault(out.seq_id, RequestOutput(out.seq_id))
-                acc.new_token_ids.extend(out.new_token_ids)
-                if out.finished:
-                    acc.finish_reason = out.finish_reason
-            steps += 1
-            if steps >= max_steps:
-                raise RuntimeError(f"Engine.run() hit max_steps ({max_steps}). Possible livelock.")
-        return final
+        """Steps until every request is done (also reporting requests that finished on arrival)."""
+        merged: dict[int, RequestOutput] = {}
+        for _ in range(max_steps):
+            if not (self.has_unfinished_requests() or self.scheduler.finished_seqs):
+                return merged
+            for o in self.step():
+                merged.setdefault(o.seq_id, RequestOutput(o.seq_id)).merge(o)
+        raise RuntimeError(f"requests still unfinished after {max_steps} steps")
 
     def reset(self) -> None:
         self.scheduler.waiting.clear()

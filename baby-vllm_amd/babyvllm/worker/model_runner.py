@@ -10,8 +10,9 @@
   and context inside BATCH_BUCKETS × CTX_BUCKETS, replays a hipGraph captured
   once per (batch bucket, context bucket): the whole forward, the LM head into
   a static logits buffer and the greedy argmax kernel into a static token
-  buffer. Its inputs come from ``DecodeInputs`` staging (pinned host arrays
-  edited in place) by non-blocking copies; the attention kernels see
+  buffer. Its inputs come from ``DecodeInputs`` staging (one pinned buffer
+  edited in place) by a single non-blocking copy into a device buffer of the
+  same layout, which every captured graph reads; the attention kernels see
   ``max_seq_len`` = the context bucket, so the captured grid fits every replay.
 * Any other step runs eagerly with metadata built from the scheduler output,
   then takes each sequence's last row of hidden states to the LM head.
@@ -82,6 +83,8 @@ class ModelRunner:
         self._graphs: dict[tuple[int, int], torch.cuda.CUDAGraph] = {}
         self._pool = None
         self._decode_inputs: DecodeInputs | None = None
+        self._dev_packed: torch.Tensor | None = None
+        self._dev_inputs: dict[str, torch.Tensor] | None = None
         # Observability for tests and benchmarks: decode steps served by a graph
         # replay, and an optional callable(seqs, logits) shown every step's
         # logits rows (row i belongs to seqs[i]) before sampling.
@@ -192,14 +195,17 @@ class ModelRunner:
         key = (batch_bucket, ctx_bucket)
         if key not in self._static:
             B, dev = batch_bucket, self.device
+            host = self._host_inputs()
+            if self._dev_inputs is None:
+                # One device buffer with the host staging's packed layout: a step's
+                # inputs arrive by a single copy, and every graph reads its rows.
+                self._dev_packed = torch.zeros(host.packed.numel(), dtype=torch.uint8, device=dev)
+                self._dev_inputs = host.device_views(self._dev_packed)
+            v = self._dev_inputs
             self._static[key] = StaticBuffers(
-                input_ids=torch.zeros(B, dtype=torch.int64, device=dev),
-                position_ids=torch.zeros(B, dtype=torch.int64, device=dev),
-                block_tables=torch.full((B, self.max_blocks_per_seq), self._dummy_block, dtype=torch.int32,
-                                        device=dev),
-                seq_lens=torch.zeros(B, dtype=torch.int32, device=dev),
-                context_lens=torch.zeros(B, dtype=torch.int32, device=dev),
-                slot_mapping=torch.full((B,), self._dummy_block * self.block_size, dtype=torch.int64, device=dev),
+                input_ids=v["input_ids"][:B], position_ids=v["positions"][:B],
+                block_tables=v["block_tables"][:B], seq_lens=v["seq_lens"][:B],
+                context_lens=v["context_lens"][:B], slot_mapping=v["slot_mapping"][:B],
                 query_start_loc=torch.arange(B + 1, dtype=torch.int32, device=dev),
                 logits=torch.zeros(B, self.model_config.vocab_size, dtype=self.dtype, device=dev),
                 tokens=torch.zeros(B, dtype=torch.int64, device=dev),
@@ -216,11 +222,7 @@ class ModelRunner:
         buf = self._ensure_static_buffers(batch_bucket, ctx_bucket)
         host = self._host_inputs()
         host.update(seqs, block_tables, batch_bucket)
-        B = batch_bucket
-        for dst, src in ((buf.input_ids, host.t_input_ids), (buf.position_ids, host.t_positions),
-                         (buf.seq_lens, host.t_seq_lens), (buf.context_lens, host.t_context_lens),
-                         (buf.slot_mapping, host.t_slot_mapping), (buf.block_tables, host.t_block_tables)):
-            dst.copy_(src[:B], non_blocking=True)
+        self._dev_packed.copy_(host.packed, non_blocking=True)
         return buf
 
     @torch.inference_mode()
@@ -271,7 +273,7 @@ class ModelRunner:
             self.logits_observer(seqs, buf.logits[:n])
         if all(s.sampling_params.temperature == 0.0 for s in seqs):
             host = self._decode_inputs
-            host.t_tokens[:bb].copy_(buf.tokens, non_blocking=True)
+            host.token_buffer[:bb].copy_(buf.tokens, non_blocking=True)
             torch.cuda.current_stream(self.device).synchronize()
             return {s.seq_id: int(t) for s, t in zip(seqs, host.tokens[:n])}
         return self._sample(buf.logits[:n], seqs)

@@ -404,7 +404,7 @@ def bench_generate(n_prompts=64, prompt_len=1920, shared_len=1536, new_tokens=64
             outs = engine.step()
             now = time.perf_counter() - start
             steps += 1
-            peak_pages = max(peak_pages, len(engine.kv_cache_manager.used_block_ids))
+            peak_pages = max(peak_pages, engine.kv_cache_manager.num_used_blocks)
             for o in outs:
                 n_tokens += len(o.new_token_ids)
                 if o.new_token_ids and o.seq_id not in first:
