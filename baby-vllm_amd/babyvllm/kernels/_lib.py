@@ -97,6 +97,7 @@ TUNE_PREFILL_BLOCKS_PER_WG = 1
 TUNE_DECODE_ORDER = 2
 TUNE_DECODE_SINGLE_PASS_STREAM = 3
 TUNE_DECODE_CACHED = 4
+TUNE_APPEND_CHUNKS = 5
 
 
 class KernelLibraryError(RuntimeError):

@@ -120,7 +120,8 @@ enum TuneKnob {
   kTuneDecodeOrder = 2,             // 1: split units fastest in the streaming wave numbering (same bits)
   kTuneDecodeSinglePassStream = 3,  // 1: single-pass launches on streaming waves too (same bits)
   kTuneDecodeCached = 4,            // 1: streaming page loads without the nontemporal hint (same bits)
-  kTuneKnobs = 5,
+  kTuneAppendChunks = 5,            // 1: aligned appends on the per-chunk kernel (same bits, NaN payloads aside)
+  kTuneKnobs = 6,
 };
 int tuning(int knob);
 int set_tuning(int knob, int value);

@@ -653,6 +653,8 @@ def main():
                     help="config1 | decode_b64 | decode_b8 | decode_b1 | append | prefill | prefill:<shape> | "
                          "step | e2e | cpu")
     ap.add_argument("--calib-copy", action="store_true")
+    ap.add_argument("--tune", action="append", default=[], metavar="KNOB=VALUE",
+                    help="set a library tuning knob (bvllm_set_tuning) before measuring; repeatable")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -669,6 +671,10 @@ def main():
 
     from babyvllm.kernels import _lib
     _lib.lib()  # fail loudly now if the HIP library is missing
+    for kv in args.tune:
+        knob, value = (int(x) for x in kv.split("="))
+        if _lib.set_tuning(knob, value) < 0:
+            raise SystemExit(f"unknown tuning knob {knob}")
 
     if args.only == "config1":
         r = bench_config1(args.warmup, args.steps)

@@ -181,7 +181,8 @@ BVLLM_API int bvllm_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_s
  * column blocks per work-group (tables of at most 8 pages), 2 decode wave
  * order (1 split units fastest), 3 decode single pass on streaming waves (1),
  * 4 decode page loads of the streaming waves without the nontemporal hint
- * (1). No knob changes any result bit.
+ * (1), 5 aligned RoPE + append on the per-chunk kernel instead of the
+ * per-row kernel (1). No knob changes any result bit (a NaN's payload aside).
  */
 BVLLM_API int bvllm_set_tuning(int32_t knob, int32_t value);
 

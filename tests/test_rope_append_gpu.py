@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from oracle import rope as orope
-from tests._cases import BLOCK_SIZE
+from tests._cases import BLOCK_SIZE, tuned
 
 pytestmark = [
     pytest.mark.gpu,
@@ -211,3 +211,67 @@ def test_random_steps_bitwise(seed):
     assert _bits_equal(q, qr) and _bits_equal(k, kr)
     if with_cache:
         assert _bits_equal(cache, cr)
+
+
+# The two aligned append kernels (bvllm_set_tuning knob 5): 0 = head rows per
+# wave (the default), 1 = one thread per 16-byte chunk pair. Same bits.
+_LAYOUTS = [0, 1]
+
+
+def _special_values(n, g):
+    """bf16 values that stress rounding: ±inf, NaN of both signs, the largest
+    finite values, subnormals, signed zeros and ordinary normals."""
+    special = torch.tensor([float("inf"), float("-inf"), float("nan"), -float("nan"),
+                            3.3895e38, -3.3895e38, 1e-39, -1e-39, 9.2e-41, 0.0, -0.0, 1.0],
+                           dtype=torch.float32).bfloat16()
+    x = torch.randn(n, generator=g).bfloat16()
+    pick = torch.randint(0, 3, (n,), generator=g) == 0
+    x[pick] = special[torch.randint(0, special.numel(), (int(pick.sum()),), generator=g)]
+    return x
+
+
+@pytest.mark.parametrize("layout", _LAYOUTS)
+def test_special_values_bitwise(layout):
+    """inf, NaN, overflow and subnormal inputs (q, k, cos, sin): NaN exactly where
+    the oracle has NaN, every other output bit equal to the oracle's. (A NaN's
+    sign and payload are not compared: torch's own CPU kernels store 0x7fc0 on
+    their scalar path and 0xffff on their vector path.)"""
+    T, H, Hkv, D = 24, 28, 4, 128
+    g = torch.Generator().manual_seed(11)
+    q = _special_values(T * H * D, g).view(T, H, D).cuda()
+    k = _special_values(T * Hkv * D, g).view(T, Hkv, D).cuda()
+    v = _special_values(T * Hkv * D, g).view(T, Hkv, D).cuda()
+    cos = _special_values(T * D, g).view(T, D).cuda()
+    sin = _special_values(T * D, g).view(T, D).cuda()
+    cache = torch.zeros(2, 4, BLOCK_SIZE, Hkv, D, device="cuda", dtype=torch.bfloat16)
+    slots = torch.randperm(4 * BLOCK_SIZE, generator=g)[:T].to(torch.int64).cuda()
+    qr, kr, cr = _oracle(q, k, v, cos, sin, cache, slots)
+    with tuned(5, layout):
+        _kernel()(q, k, v, cos, sin, cache, slots)
+        torch.cuda.synchronize()
+    for got, want in ((q, qr), (k, kr), (cache, cr)):
+        got, want = got.cpu(), want.cpu()
+        nan = want.isnan()
+        assert torch.equal(got.isnan(), nan)
+        assert torch.equal(got[~nan].view(torch.int16), want[~nan].view(torch.int16))
+
+
+@pytest.mark.parametrize("layout", _LAYOUTS)
+@pytest.mark.parametrize("H,Hkv,D,T", [(28, 4, 128, 37), (14, 2, 64, 9), (8, 8, 128, 5), (4, 4, 256, 3),
+                                       (32, 8, 128, 2), (12, 2, 64, 1)])
+def test_layouts_give_the_same_bits(layout, H, Hkv, D, T):
+    _, q, k, v = _qkv(T, H, Hkv, D, seed=T)
+    g = torch.Generator(device="cuda").manual_seed(T + 1)
+    cos = torch.randn(T, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    sin = torch.randn(T, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    nb = (T + BLOCK_SIZE - 1) // BLOCK_SIZE + 2
+    cache = torch.randn(2, nb, BLOCK_SIZE, Hkv, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    slots = torch.randperm(nb * BLOCK_SIZE, device="cuda", generator=g)[:T].to(torch.int64)
+    slots[0] = -1  # out-of-range slot: not written
+    qr, kr, _ = _oracle(q, k, v, cos, sin, None, None)
+    cr = cache.cpu().clone()
+    orope.store_kvcache(kr[1:], v.cpu()[1:], cr, slots.cpu()[1:])
+    with tuned(5, layout):
+        _kernel()(q, k, v, cos, sin, cache, slots)
+        torch.cuda.synchronize()
+    assert _bits_equal(q, qr) and _bits_equal(k, kr) and _bits_equal(cache, cr)
