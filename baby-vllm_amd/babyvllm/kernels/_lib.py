@@ -98,6 +98,7 @@ TUNE_DECODE_ORDER = 2
 TUNE_DECODE_SINGLE_PASS_STREAM = 3
 TUNE_DECODE_CACHED = 4
 TUNE_APPEND_CHUNKS = 5
+TUNE_PREFILL_SHORT_GRID = 6
 
 
 class KernelLibraryError(RuntimeError):

@@ -121,7 +121,8 @@ enum TuneKnob {
   kTuneDecodeSinglePassStream = 3,  // 1: single-pass launches on streaming waves too (same bits)
   kTuneDecodeCached = 4,            // 1: streaming page loads without the nontemporal hint (same bits)
   kTuneAppendChunks = 5,            // 1: aligned appends on the per-chunk kernel (same bits, NaN payloads aside)
-  kTuneKnobs = 6,
+  kTunePrefillShortGrid = 6,        // 1: short prefill grids on the single key walk instead of the key split
+  kTuneKnobs = 7,
 };
 int tuning(int knob);
 int set_tuning(int knob, int value);

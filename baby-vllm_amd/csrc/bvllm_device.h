@@ -135,4 +135,12 @@ __device__ __forceinline__ uint4 ld16_nt(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 16-byte store with the nontemporal hint, for data the kernel writes once and
+// no later work of the same kernel reads.
+__device__ __forceinline__ void st16_nt(void* p, uint4 v) {
+  typedef uint32_t u32x4_nt __attribute__((ext_vector_type(4)));
+  const u32x4_nt w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4_nt*>(p));
+}
+
 }  // namespace bvllm

@@ -9,7 +9,9 @@
 // query-major (f = query·G + head), so every K/V tile is staged once per
 // work-group and shared by the whole GQA group, and every MFMA column holds a
 // pair whatever G is (a 16-column tile may span queries: the causal limit is
-// per column). Each of the NW waves owns QT 16-column tiles; CB = NW·QT·16.
+// per column). Each of the NW waves owns QT 16-column tiles; CB = NW·QT·16
+// (with the key split KS = 2, below: pairs of waves share their tiles and each
+// takes one half of every key tile; CB = NW/2·QT·16).
 // Keys come in tiles of 64 (four 16-token pages), moved from the cache into LDS
 // by direct global->LDS loads (no staging registers), rows XOR-swizzled instead
 // of padded. K and V each have two LDS buffers; K runs one tile ahead of V.
@@ -90,7 +92,12 @@ constexpr int kDecodeDepth = 2;
 
 // MB: groups of several blocks per work-group, launched only when every
 // sequence's keys fit two 64-key tiles (the kernel has no streaming path then).
-template <int D, int NW, int QT, bool MB>
+// KS: key split inside the work-group. KS = 1: each wave owns QT column tiles
+// and walks every key. KS = 2: the waves form NW/2 column groups of QT tiles,
+// and the two waves of a group take the two 32-key halves of every 64-key tile
+// (twice the columns per LDS read of K and V and per staged tile, for the same
+// waves); their partial states merge through LDS at the end.
+template <int D, int NW, int QT, bool MB, int KS>
 __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a, int n_blocks_bound, int dense_qb,
                                                                   int xcd_group, int per_xcd, DecodeArgs dec,
                                                                   int n_dec_wgs, int bpw) {
@@ -125,7 +132,8 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   }
 
   const int G = a.num_heads / a.num_kv_heads;
-  constexpr int CB = NW * QT * 16;  // columns of a work-group's block
+  static_assert(KS == 1 || (KS == 2 && !MB && NW % 2 == 0), "key split: two halves, streaming path only");
+  constexpr int CB = NW / KS * QT * 16;  // columns of a work-group's block
 
   // Work-groups are dispatched round-robin over the 8 XCDs (XCD = id mod 8).
   // xcd_group == -1 (many (sequence, KV head) pairs, dense numbering): each XCD
@@ -197,14 +205,16 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
     for (int pg = 0; pg < PAGES_PER_TILE; ++pg)
       po[pg] = (int64_t)((uint64_t)(uint32_t)min(max(raw[pg], 0), a.num_pages - 1) * page_bytes);
   };
-  int64_t po_v[PAGES_PER_TILE], po_k[PAGES_PER_TILE];
+  int64_t po_v[PAGES_PER_TILE], po_k[PAGES_PER_TILE], po_n[PAGES_PER_TILE];
   {
-    int raw0[PAGES_PER_TILE], raw1[PAGES_PER_TILE];
+    int raw0[PAGES_PER_TILE], raw1[PAGES_PER_TILE], raw2[PAGES_PER_TILE];
     page_fetch(0, raw0);
     page_fetch(1, raw1);
+    if constexpr (KS == 2) page_fetch(2, raw2);
     asm volatile("" : "+s"(q_start), "+s"(q_end), "+s"(seq_len), "+s"(ctx));
     page_finish(raw0, po_v);
     page_finish(raw1, po_k);
+    if constexpr (KS == 2) page_finish(raw2, po_n);
   }
   const int q_len = q_end - q_start;
   const int n_cols = q_len * G;
@@ -222,6 +232,8 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   const int n = lane & 15;
   const int g = lane >> 4;
   const int w = wave_id();
+  const int cw = w % (NW / KS);  // the wave's column group
+  const int kh = w / (NW / KS);  // KS = 2: the 32-key half of every tile the wave takes
 
   bool kv_staged = false;
   int blk = b_last;
@@ -234,7 +246,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
 
   // The wave's columns: f = wave_f0 + 16·ct + n of the block's flat
   // (query, head) numbering, query f / G and head f mod G.
-  const int wave_f0 = blk * CB + w * QT * 16;
+  const int wave_f0 = blk * CB + cw * QT * 16;
   const int wave_q0 = wave_f0 / G;  // first query index of this wave
   const bool wave_live = wave_f0 < n_cols;
   const int wave_hi = ctx + min(q_len - 1, (wave_f0 + QT * 16 - 1) / G);  // last visible key position
@@ -353,6 +365,9 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   // 32-key halves of tiles this wave computes: up to its last visible key
   // (wave_hi) and below hi.
   const int wave_halves = wave_live ? min((hi + 31) / 32, wave_hi / 32 + 1) : 0;
+  // KS = 2: tiles whose half kh holds a key this wave's columns see.
+  const int wave_last_key = min(wave_hi, hi - 1);
+  const int wave_tiles = (KS == 2 && wave_live && wave_last_key >= 32 * kh) ? (wave_last_key - 32 * kh) / 64 + 1 : 0;
 
   // ---- products and softmax, per 32-key half of a 64-key tile ----
   // Sᵀ of keys 32h .. 32h+31 of the tile in K buffer kbuf, for the wave's QT
@@ -495,18 +510,27 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   // Loads are waited for in issue order (vmcnt), one tile step after issue;
   // the last steps load tiles past n_tiles (clamped table entries, in bounds)
   // that are never read, so the steady state has no branches around loads.
-  const bool short_wg = MB || n_tiles <= 2;
+  // KS = 2 (a wave takes half kh of every tile): the prologue loads K(0),
+  // V(0), K(1) and computes Sᵀ(0); step j then loads V(j+1) and K(j+2) (their
+  // buffers' previous tiles were consumed in step j-1), computes Sᵀ(j+1) from
+  // K(j+1) while forming P(j), accumulates PV(j), waits for its loads, clears
+  // V(j+1)'s rows past hi and ends with the one barrier of the step. The
+  // page numbers of tile j+3 are fetched under step j's products.
+  const bool short_wg = KS == 1 && (MB || n_tiles <= 2);
   f32x4_t S0[QT][2], S1[QT][2];
   if (n_tiles > 0 && !(kv_staged && short_wg)) {
     stage_k(po_v, 0);
     stage_v(po_v, 0);
     if (n_tiles > 1 || !short_wg) stage_k(po_k, 1);
-    if (n_tiles == 2) stage_v(po_k, 1);
+    if (short_wg && n_tiles == 2) stage_v(po_k, 1);
     wait_loads();
     zero_v_tail(0, 0);
-    if (n_tiles == 2) zero_v_tail(1, 1);
+    if (short_wg && n_tiles == 2) zero_v_tail(1, 1);
 #pragma unroll
-    for (int pg = 0; pg < PAGES_PER_TILE; ++pg) po_v[pg] = po_k[pg];
+    for (int pg = 0; pg < PAGES_PER_TILE; ++pg) {
+      po_v[pg] = po_k[pg];
+      if constexpr (KS == 2) po_k[pg] = po_n[pg];
+    }
   }
   kv_staged = short_wg;
   // The Q loads complete here, once, after the first tiles' table fetch and
@@ -517,9 +541,9 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
 #pragma unroll
     for (int c = 0; c < KC; ++c) asm volatile("" ::"v"(qreg[ct][c].x), "v"(qreg[ct][c].y), "v"(qreg[ct][c].z), "v"(qreg[ct][c].w));
   __syncthreads();
-  if (wave_halves > 0) {
-    qk(S0, 0, 0);
-    if (needs_mask(0)) mask(S0, 0);
+  if (KS == 1 ? wave_halves > 0 : wave_tiles > 0) {
+    qk(S0, 0, KS == 2 ? kh : 0);
+    if (needs_mask(32 * kh)) mask(S0, 32 * kh);
     // The first half's max is the first reference; a column with no visible
     // key yet takes 0 (its P is then 0, and a later max above 8 raises it).
     float mt[QT];
@@ -527,6 +551,9 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
 #pragma unroll
     for (int ct = 0; ct < QT; ++ct) m[ct] = mt[ct] == kNegInf ? 0.f : mt[ct];
   }
+  // KS = 2: step 0 loads K(2) into K(0)'s buffer, which every wave has just
+  // read for Sᵀ(0).
+  if constexpr (KS == 2) __syncthreads();
 
   // Half step x (= 2j + h) on S(x) in Sc, producing S(x+1) in Sn.
   auto half_step = [&](const int x, f32x4_t (&Sc)[QT][2], f32x4_t (&Sn)[QT][2], const int kbuf_next,
@@ -570,7 +597,75 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
 #pragma unroll
     for (int pg = 0; pg < PAGES_PER_TILE; ++pg) po_v[pg] = po_k[pg];
   };
-  if (short_wg) {
+  // KS = 2: tile step j (b = j & 1) on Sᵀ(j) in Sc, producing Sᵀ(j+1) in Sn.
+  auto split_step = [&](const int j, const int b, f32x4_t (&Sc)[QT][2], f32x4_t (&Sn)[QT][2])
+                        __attribute__((always_inline)) {
+    stage_v(po_v, b ^ 1);  // V(j+1)
+    stage_k(po_k, b);      // K(j+2)
+    int raw[PAGES_PER_TILE];
+    page_fetch(j + 3, raw);
+    if (j < wave_tiles) {
+      uint4 pb[QT];
+      __builtin_amdgcn_s_setprio(1);
+      qk(Sn, b ^ 1, kh);
+      softmax_p(Sc, pb);
+#pragma unroll
+      for (int ct = 0; ct < QT; ++ct) asm volatile("" ::"v"(pb[ct].x), "v"(pb[ct].y), "v"(pb[ct].z), "v"(pb[ct].w));
+      __builtin_amdgcn_s_setprio(0);
+      raise_max(Sc, pb);
+      if (needs_mask(64 * (j + 1) + 32 * kh)) mask(Sn, 64 * (j + 1) + 32 * kh);
+      __builtin_amdgcn_s_setprio(1);
+      pv(pb, b, kh);
+      __builtin_amdgcn_s_setprio(0);
+    }
+    page_finish(raw, po_n);
+    wait_loads();
+    zero_v_tail(j + 1, b ^ 1);
+    __syncthreads();
+#pragma unroll
+    for (int pg = 0; pg < PAGES_PER_TILE; ++pg) {
+      po_v[pg] = po_k[pg];
+      po_k[pg] = po_n[pg];
+    }
+  };
+  if constexpr (KS == 2) {
+    for (int j = 0; j < n_tiles; j += 2) {
+      split_step(j, 0, S0, S1);
+      if (j + 1 < n_tiles) split_step(j + 1, 1, S1, S0);
+    }
+    // Wave kh = 1 hands its state (reference max, row sums, accumulators) to
+    // wave kh = 0 of its column group through LDS, free after the last
+    // step's barrier; the receiver rescales both to the larger reference.
+    static_assert((NW / KS) * (QT * 64 * 2 + QT * VD * 64 * 4) * 4 <= (int)sizeof(lds), "merge fits the tile buffers");
+    float* xs = reinterpret_cast<float*>(lds) + cw * (QT * 64 * 2 + QT * VD * 64 * 4);
+    if (kh == 1) {
+#pragma unroll
+      for (int ct = 0; ct < QT; ++ct) {
+        xs[ct * 64 + lane] = m[ct];
+        xs[(QT + ct) * 64 + lane] = lsum[ct][0];
+#pragma unroll
+        for (int c = 0; c < VD; ++c)
+          *reinterpret_cast<f32x4_t*>(xs + QT * 64 * 2 + ((ct * VD + c) * 64 + lane) * 4) = acc[ct][c];
+      }
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+      for (int ct = 0; ct < QT; ++ct) {
+        const float m2 = xs[ct * 64 + lane];
+        const float l2 = xs[(QT + ct) * 64 + lane];
+        const float mm = fmax_prop(m[ct], m2);
+        const float a1 = mm == kNegInf ? 0.f : fast_exp2(m[ct] - mm);
+        const float a2 = mm == kNegInf ? 0.f : fast_exp2(m2 - mm);
+        lsum[ct][0] = lsum[ct][0] * a1 + l2 * a2;
+#pragma unroll
+        for (int c = 0; c < VD; ++c) {
+          const f32x4_t o2 = *reinterpret_cast<const f32x4_t*>(xs + QT * 64 * 2 + ((ct * VD + c) * 64 + lane) * 4);
+          acc[ct][c] = acc[ct][c] * a1 + o2 * a2;
+        }
+      }
+    }
+  } else if (short_wg) {
     // Every tile is in LDS; the last half's Sᵀ(x+1) reads K buffer 0 (in
     // bounds, never used).
     half_step(0, S0, S1, 0, 1, 0, 0);
@@ -607,7 +702,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
       const uint32_t y1 = pack_bf16x2_hw(acc[ct][c + 1][2] * inv, acc[ct][c + 1][3] * inv);
       const auto sx = __builtin_amdgcn_permlane16_swap(x0, x1, false, false);
       const auto sy = __builtin_amdgcn_permlane16_swap(y0, y1, false, false);
-      if (valid[ct]) st16(orow + 16 * c, make_uint4(sx[0], sy[0], sx[1], sy[1]));
+      if (valid[ct] && kh == 0) st16(orow + 16 * c, make_uint4(sx[0], sy[0], sx[1], sy[1]));
     }
   }
   if (!MB) break;
@@ -673,18 +768,21 @@ static PrefillGrid plan_prefill(const PrefillArgs& a, int64_t CB) {
   return p;
 }
 
-template <int D, int NW, int QT>
+template <int D, int NW, int QT, int KS = 1>
 static hipError_t launch_prefill(const PrefillArgs& a, const PrefillGrid& p, int bpw, hipStream_t stream) {
   if (p.prefill_wgs + p.dec_wgs == 0) return hipSuccess;
   if (p.prefill_wgs + p.dec_wgs > 0x7ffffff0) return hipErrorInvalidValue;
-  if (bpw > 1)
-    hipLaunchKernelGGL((paged_prefill_kernel<D, NW, QT, true>), dim3((unsigned)(p.dec_wgs + p.prefill_wgs)),
-                       dim3(NW * 64), 0, stream, a, (int)p.bound, p.dense_qb, p.xcd_group, (int)p.per_xcd,
-                       single_query_view(a), (int)p.dec_wgs, bpw);
-  else
-    hipLaunchKernelGGL((paged_prefill_kernel<D, NW, QT, false>), dim3((unsigned)(p.dec_wgs + p.prefill_wgs)),
-                       dim3(NW * 64), 0, stream, a, (int)p.bound, p.dense_qb, p.xcd_group, (int)p.per_xcd,
-                       single_query_view(a), (int)p.dec_wgs, 1);
+  if constexpr (KS == 1) {
+    if (bpw > 1) {
+      hipLaunchKernelGGL((paged_prefill_kernel<D, NW, QT, true, 1>), dim3((unsigned)(p.dec_wgs + p.prefill_wgs)),
+                         dim3(NW * 64), 0, stream, a, (int)p.bound, p.dense_qb, p.xcd_group, (int)p.per_xcd,
+                         single_query_view(a), (int)p.dec_wgs, bpw);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((paged_prefill_kernel<D, NW, QT, false, KS>), dim3((unsigned)(p.dec_wgs + p.prefill_wgs)),
+                     dim3(NW * 64), 0, stream, a, (int)p.bound, p.dense_qb, p.xcd_group, (int)p.per_xcd,
+                     single_query_view(a), (int)p.dec_wgs, 1);
   return hipGetLastError();
 }
 
@@ -710,9 +808,11 @@ static int prefill_blocks_per_wg(const PrefillArgs& a, const PrefillGrid& p1) {
 
 // Two column tiles per wave (128 columns per work-group) unless that grid
 // gives fewer than two prefill work-groups per CU (short batches, mixed
-// steps): then one tile per wave, 64 columns per work-group, twice the
-// work-groups (mixed 1 x 512 + 63 decodes: 39.5 -> 34.4 us; 8 x (1024 + 128):
-// 34.7 -> 33.2 us).
+// steps): then 64 columns per work-group, twice the work-groups, computed by
+// the key split (two column groups of two waves, each wave on one half of
+// every key tile; 8 x (1024 + 128): 29.4-29.9 us against 31.3-31.7 us for one
+// column tile per wave over every key, the choice behind the tuning switch
+// kTunePrefillShortGrid; mixed 1 x 512 + 63 decodes: 29.3-30.0 us either way).
 template <int D>
 static hipError_t prefill_for_dim(const PrefillArgs& a, hipStream_t stream) {
   const PrefillGrid p2 = plan_prefill(a, 4 * 2 * 16);
@@ -721,7 +821,8 @@ static hipError_t prefill_for_dim(const PrefillArgs& a, hipStream_t stream) {
     if (bpw == 1) return launch_prefill<D, 4, 2>(a, p2, 1, stream);
     return launch_prefill<D, 4, 2>(a, plan_prefill(a, 4 * 2 * 16 * (int64_t)bpw), bpw, stream);
   }
-  return launch_prefill<D, 4, 1>(a, plan_prefill(a, 4 * 1 * 16), 1, stream);
+  if (tuning(kTunePrefillShortGrid) == 1) return launch_prefill<D, 4, 1>(a, plan_prefill(a, 4 * 1 * 16), 1, stream);
+  return launch_prefill<D, 4, 2, 2>(a, plan_prefill(a, 4 / 2 * 2 * 16), 1, stream);
 }
 
 hipError_t paged_prefill(const PrefillArgs& a, hipStream_t stream) {

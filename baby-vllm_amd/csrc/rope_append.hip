@@ -172,12 +172,6 @@ __device__ __forceinline__ void to_floats(const uint4& c, float* f) {
   }
 }
 
-__device__ __forceinline__ void st16_nt(uint16_t* p, const uint4& v) {
-  typedef uint32_t u32x4_nt __attribute__((ext_vector_type(4)));
-  const u32x4_nt w = {v.x, v.y, v.z, v.w};
-  __builtin_nontemporal_store(w, reinterpret_cast<u32x4_nt*>(p));
-}
-
 template <int D>
 __global__ __launch_bounds__(256) void rope_append_rows_kernel(RopeArgs a, int32_t units) {
   constexpr int HALF = D / 2;

@@ -12,6 +12,7 @@ from oracle import attention as oa
 from tests._cases import assert_attn_close, build_prefill_case, md_to_cpu, scale_keys_by_position, tuned
 
 _BPW = 1  # tuning knob: prefill column blocks per work-group (bvllm_set_tuning)
+_SHORT_GRID = 6  # tuning knob: 1 = short grids on the single key walk instead of the key split
 
 pytestmark = [
     pytest.mark.gpu,
@@ -305,3 +306,48 @@ def test_long_sequence_with_one_key_repeated(hkv, group, d):
     expected = prefix_mean[ctx:].repeat_interleave(group, dim=1)  # [n, H, D]
     actual = _kernel()(q, kv_cache, md, d ** -0.5)
     assert_attn_close(actual, expected)
+
+
+# ------------------------------------------ in-work-group key split (short grids)
+
+KEY_SPLIT_CASES = {
+    "8x(1024+128)": [(1024, 128)] * 8,
+    "one tile, both halves": [(0, 40), (10, 50)],
+    "first half only": [(0, 20), (5, 9), (0, 1)],
+    "odd tile counts": [(100, 91), (0, 193), (311, 2)],
+    "long prefix few queries": [(3000, 5), (1500, 17)],
+}
+
+
+@pytest.mark.parametrize("name", list(KEY_SPLIT_CASES))
+@pytest.mark.parametrize("hkv,group,d", [(4, 7, 128), (2, 7, 64), (1, 16, 128)])
+def test_short_grid_kernels_match_the_oracle(name, hkv, group, d):
+    """Grids too small for two work-groups per CU at 128 columns run 64-column
+    work-groups whose two waves per column group take the two halves of every
+    key tile and merge at the end; the single key walk (one wave per column
+    tile over every key) stays behind a tuning knob. Both within tolerance of
+    the oracle, with edge cases: a sequence inside one tile, columns whose keys
+    all lie in a first half, odd tile counts, long prefixes with few queries."""
+    specs = KEY_SPLIT_CASES[name]
+    q, kv_cache, md = build_prefill_case(specs, hkv, group, d, seed=len(specs) + d)
+    expected = _oracle(q, kv_cache, md, group)
+    split = _kernel()(q, kv_cache, md, d ** -0.5)
+    with tuned(_SHORT_GRID, 1):
+        walk = _kernel()(q, kv_cache, md, d ** -0.5)
+    for out in (split, walk):
+        assert not torch.isnan(out).any()
+        assert_attn_close(out, expected)
+
+
+@pytest.mark.parametrize("growth", [6.0, 40.0])
+def test_key_split_with_rising_scores(growth):
+    """The rescale path on both halves: key norms growing with position, so the
+    two waves of a column group raise their reference maxima at different tiles
+    and the merge rescales the two partial states by different factors."""
+    specs = [(700, 60), (0, 300), (129, 2), (64, 64)]
+    q, kv_cache, md = build_prefill_case(specs, 4, 7, 128, seed=int(growth))
+    scale_keys_by_position(kv_cache, md.block_tables, md.seq_lens_cpu, lambda p: 1.0 + p / growth)
+    expected = _oracle(q, kv_cache, md, 7)
+    assert_attn_close(_kernel()(q, kv_cache, md, 128 ** -0.5), expected)
+    with tuned(_SHORT_GRID, 1):
+        assert_attn_close(_kernel()(q, kv_cache, md, 128 ** -0.5), expected)
