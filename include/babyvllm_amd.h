@@ -182,7 +182,10 @@ BVLLM_API int bvllm_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_s
  * order (1 split units fastest), 3 decode single pass on streaming waves (1),
  * 4 decode page loads of the streaming waves without the nontemporal hint
  * (1), 5 aligned RoPE + append on the per-chunk kernel instead of the
- * per-row kernel (1). No knob changes any result bit (a NaN's payload aside).
+ * per-row kernel (1), 6 short prefill grids on the single key walk instead of
+ * the in-work-group key split (1). Knobs 0-5 change no result bit (a NaN's
+ * payload aside); knob 6 changes the prefill's summation order (both paths
+ * within the same tolerance of the reference).
  */
 BVLLM_API int bvllm_set_tuning(int32_t knob, int32_t value);
 
