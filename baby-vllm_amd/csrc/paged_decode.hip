@@ -20,6 +20,16 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
   decode_work_group<D, NW, PF>(a, blockIdx.x, smem);
 }
 
+// Two waves per split (PAIR), four pages in flight each.
+template <int D, bool NT>
+__global__ __launch_bounds__(128) void paged_decode_pair_kernel(DecodeArgs a, int items) {
+  __shared__ __attribute__((aligned(16))) unsigned char tile[2 * kTileBytes<D>];
+  __shared__ __attribute__((aligned(16))) float xs[kPairLdsFloats<D>];
+  const int item = (int)blockIdx.x;
+  if (item >= items) return;
+  decode_stream_wave<D, 4, NT, false, true>(a, item, tile + wave_id() * kTileBytes<D>, xs);
+}
+
 // One streaming wave per work-group, so that a short batch's splits spread
 // over every CU.
 template <int D, int PF, bool NT, bool GROUP>
@@ -255,6 +265,7 @@ DecodePlan decode_plan(int32_t batch, int32_t num_kv_heads, int32_t num_splits, 
   p.splits_per_item = group_mode ? p.group : 1;
   p.partials = group_mode ? (int32_t)groups : num_splits;
   p.fold_in_reduce = !group_mode && p.group > 1;
+  p.pair = !group_mode && forced != 1;
   return p;
 }
 
@@ -353,8 +364,18 @@ static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
   const int64_t units = (a.num_splits + a.splits_per_item - 1) / a.splits_per_item;
   const int64_t items = (int64_t)a.batch * a.num_kv_heads * units;
   if (items > 0x7ffffff0) return hipErrorInvalidValue;
-  hipError_t err = a.splits_per_item > 1 ? launch_stream<D, true>(a, items, stream)
-                                         : launch_stream<D, false>(a, items, stream);
+  hipError_t err;
+  if (a.splits_per_item > 1) {
+    err = launch_stream<D, true>(a, items, stream);
+  } else if (p.pair) {
+    if (tuning(kTuneDecodeCached) == 0)
+      hipLaunchKernelGGL((paged_decode_pair_kernel<D, true>), dim3((unsigned)items), dim3(128), 0, stream, a, (int)items);
+    else
+      hipLaunchKernelGGL((paged_decode_pair_kernel<D, false>), dim3((unsigned)items), dim3(128), 0, stream, a, (int)items);
+    err = hipGetLastError();
+  } else {
+    err = launch_stream<D, false>(a, items, stream);
+  }
   if (err != hipSuccess || p.single_pass) return err;
   return launch_reduce<D>(a, p, stream);
 }

@@ -74,12 +74,21 @@ __device__ __forceinline__ float group_lse(const GroupFold& f) { return f.L > 0.
 // One streaming decode wave: item = (row, KV head, unit of a.splits_per_item
 // consecutive splits); `tile` is the wave's K transpose tile (kTileBytes<D>
 // bytes of LDS).
-template <int D, int PF, bool NT, bool GROUP>
-__device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const int item, unsigned char* tile) {
+// PAIR: the item's work-group has two waves; wave w holds states 2w and 2w+1
+// of the split (its pages 4k + 2w and 4k + 2w + 1), with four pages in flight
+// instead of two, and hands its states to wave 0 through `xs` (kPairLdsFloats<D>
+// floats of LDS), which merges the four in order as a single wave would.
+template <int D>
+constexpr int kPairLdsFloats = 2 * (2 + 4 * (D / 16)) * 64;
+
+template <int D, int PF, bool NT, bool GROUP, bool PAIR = false>
+__device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const int item, unsigned char* tile,
+                                                   float* xs = nullptr) {
   constexpr int KC = D / 32;
   constexpr int VD = D / 16;
   constexpr int OPL = D / 4;  // output floats per lane: head n, dims VD·(4g+i) + c
-  static_assert(PF == 2, "pages in flight per wave");
+  static_assert((!PAIR && PF == 2) || (PAIR && PF == 4 && !GROUP), "pages in flight per wave");
+  const int w = PAIR ? wave_id() : 0;
 
   const int G = a.num_heads / a.num_kv_heads;
   const int S = a.num_splits;
@@ -231,6 +240,30 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
     const int slot_ent = min(max(ent, 0), a.num_pages - 1);
     auto phys = [&](int k) -> int64_t { return (int64_t)__builtin_amdgcn_readlane(slot_ent, k); };
     PageRegs<D> r[PF];
+    if constexpr (PAIR) {
+      // The wave's pages in order: q = 8j + 4(i/2) + 2w + (i mod 2) for ring
+      // slot i, state i mod 2 (global state 2w + i mod 2).
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        const int64_t p = phys(min(4 * (i >> 1) + 2 * w + (i & 1), here - 1)) * a.c_sb;
+        load_page<D, NT>(r[i], kc + p, vc + p, off);
+      }
+      for (int k = 0; k < here; k += 8) {
+#pragma unroll
+        for (int i = 0; i < PF; ++i) {
+          wait_page<(PF - 1) * kLoadsPerPage, D>(r[i]);
+          const int q = k + 4 * (i >> 1) + 2 * w + (i & 1);
+          if (q < here)
+            process_page<D>(st[i & 1], r[i], qb, tile, n, g, (p0 + base + q) * 16 + 4 * g, seq_len, a.scale_log2);
+          const int64_t pn = phys(min(q + 8, here - 1)) * a.c_sb;
+          load_page<D, NT>(r[i], kc + pn, vc + pn, off);
+        }
+        any = true;
+      }
+#pragma unroll
+      for (int i = 0; i < PF; ++i) wait_page<0, D>(r[i]);
+      continue;
+    }
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int64_t p = phys(min(i, here - 1)) * a.c_sb;
@@ -260,6 +293,29 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
     // are reused.
 #pragma unroll
     for (int i = 0; i < PF; ++i) wait_page<0, D>(r[i]);
+  }
+  if constexpr (PAIR) {
+    // Wave 1's states become states 2 and 3 of wave 0.
+    if (w == 1) {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        float* rec = xs + s2 * (2 + 4 * VD) * 64;
+        rec[lane] = st[s2].m;
+        rec[64 + lane] = st[s2].l;
+#pragma unroll
+        for (int c = 0; c < VD; ++c) *reinterpret_cast<f32x4_t*>(rec + 128 + (c * 64 + lane) * 4) = st[s2].acc[c];
+      }
+    }
+    __syncthreads();
+    if (w == 1) return;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const float* rec = xs + s2 * (2 + 4 * VD) * 64;
+      st[2 + s2].m = rec[lane];
+      st[2 + s2].l = rec[64 + lane];
+#pragma unroll
+      for (int c = 0; c < VD; ++c) st[2 + s2].acc[c] = *reinterpret_cast<const f32x4_t*>(rec + 128 + (c * 64 + lane) * 4);
+    }
   }
   // The split holding the unit's last pages (for a unit of one split, also
   // when it has no page: its partial is written as empty).

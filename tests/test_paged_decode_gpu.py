@@ -208,8 +208,9 @@ def test_reduce_bits_do_not_depend_on_the_split_count(n, monkeypatch):
 
 def _modes(q, kv_cache, bt, seq_lens, scale, bucket, partition):
     """Outputs of every launch choice that must give the same bits: split mode
-    (one wave per split, one wave per group of 4 splits), wave order,
-    nontemporal page loads, single pass on streaming waves."""
+    (two waves per split by default, one wave per split, one wave per group of
+    4 splits), wave order, nontemporal page loads, single pass on streaming
+    waves."""
     from babyvllm.kernels import _lib
 
     outs = {}
@@ -230,9 +231,10 @@ def _modes(q, kv_cache, bt, seq_lens, scale, bucket, partition):
 @pytest.mark.parametrize("partition", [None, 0, 1, 2, 3, 4, 7, 8, 16])
 @pytest.mark.parametrize("lens", [[600, 37, 0, 1], [2047, 16, 64, 300], [5000, 129], [130, 129, 128, 127]])
 def test_launch_choices_do_not_change_bits(partition, lens, monkeypatch):
-    """Every launch choice of one plan gives identical bits: one wave per
-    split (groups of 4 splits folded in the reduce) or per group (folded in
-    the wave), either wave order, with or without the nontemporal hint, and the single pass on work-groups or streaming waves.
+    """Every launch choice of one plan gives identical bits: two waves or one
+    wave per split (groups of 4 splits folded in the reduce) or one per group
+    (folded in the wave), either wave order, with or without the nontemporal
+    hint, and the single pass on work-groups or streaming waves.
     Rows longer than the bucket and rows ending inside a group are covered."""
     from babyvllm.kernels.decode_split import DECODE_PARTITION_ENV
 
