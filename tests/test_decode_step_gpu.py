@@ -87,6 +87,43 @@ def test_nan_is_the_maximum_and_the_first_nan_wins():
     assert torch.equal(out.cpu(), ds.greedy_argmax(x.cpu()))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_ties_nan_and_infinities_across_batches(dtype):
+    """Full-width rows: ties in different chunks go to the lowest column, a NaN
+    in a later chunk beats a larger number earlier, a negative NaN counts as
+    NaN, an all -inf row gives 0, -0.0 ties +0.0, and maxima straddling
+    power-of-two column boundaries resolve to the lower column."""
+    vocab = 152064
+    x = torch.randn(8, vocab, device="cuda", dtype=dtype)
+    x[0, [140000, 70000, 65535]] = 50.0                 # three chunks; the first wins
+    x[1, 3] = 60.0
+    x[1, 150000] = float("nan")                         # NaN in the last chunk beats 60
+    x[2, [65536, 100]] = -float("nan")                  # negative NaNs: the first wins
+    x[3] = -float("inf")                                # all -inf: column 0
+    x[4] = -1.0
+    x[4, [99999, 7]] = -0.0
+    x[4, 50000] = 0.0                                   # -0.0 ties +0.0: the lowest column
+    x[5, vocab - 1] = 70.0                              # last column
+    x[6, [32767, 32768]] = 80.0
+    x[7, [65535, 65536]] = 90.0
+    out = torch.empty(8, dtype=torch.int64, device="cuda")
+    _argmax()(x, out)
+    assert out.tolist() == [65535, 150000, 100, 0, 7, vocab - 1, 32767, 65535]
+    assert torch.equal(out.cpu(), ds.greedy_argmax(x.cpu()))
+
+
+def test_unaligned_rows_take_the_two_stage_path_with_the_same_answers():
+    vocab = 20001                                       # 40,002 bytes per row: not 16-byte aligned
+    x = torch.zeros(4, vocab, device="cuda", dtype=torch.bfloat16)
+    x[0, [8191, 8192]] = 3.0
+    x[1, [12000, 8200]] = 3.0
+    x[2, 20000] = float("nan")
+    out = torch.empty(4, dtype=torch.int64, device="cuda")
+    _argmax()(x, out)
+    assert out.tolist() == [8191, 8200, 20000, 0]
+    assert torch.equal(out.cpu(), ds.greedy_argmax(x.cpu()))
+
+
 # -------------------------------------------------------------------- RMSNorm
 
 def _rms():
