@@ -6,13 +6,23 @@ context and a cache, a step whose ``max_query_len == 1`` runs
 any longer step runs ``paged_prefill_attention``. This build has no torch
 attention path: a call on a non-ROCm tensor, without a KV cache or without a
 forward context raises instead of silently computing elsewhere.
+
+``BABYVLLM_PREFILL_ATTN`` is the reference's switch for multi-token steps
+(babyvllm/layers/attention.py:10-12,58): ``"triton"`` (its default, the paged
+prefill kernel; here the HIP kernel) or ``"hip"`` selects the kernel; the
+reference's ``"torch"`` (its per-sequence SDPA loop) is not part of this build
+and raises when a multi-token step reaches it.
 """
 
 from __future__ import annotations
 
+import os
+
 import torch.nn as nn
 
 from babyvllm.worker.context import get_forward_context
+
+_PREFILL_BACKEND = os.environ.get("BABYVLLM_PREFILL_ATTN", "triton")
 
 
 class Attention(nn.Module):
@@ -41,5 +51,9 @@ class Attention(nn.Module):
             from babyvllm.kernels.paged_attn import paged_decode_attention
             return paged_decode_attention(q, self.kv_cache, md.block_tables, md.seq_lens,
                                           self.scale, max_seq_len=md.max_seq_len)
+        if _PREFILL_BACKEND not in ("triton", "hip"):
+            raise RuntimeError(
+                f"BABYVLLM_PREFILL_ATTN={_PREFILL_BACKEND!r}: this build runs multi-token steps only on its "
+                "HIP paged prefill kernel ('triton' or 'hip'); the reference's torch SDPA loop is not shipped")
         from babyvllm.kernels.paged_prefill import paged_prefill_attention
         return paged_prefill_attention(q, self.kv_cache, md, self.scale)

@@ -91,6 +91,35 @@ def test_attention_layer_routes_to_the_hip_kernels(monkeypatch):
     assert_attn_close(out1, _oracle(q1, kv1, md1, group))
 
 
+def test_prefill_backend_switch(monkeypatch):
+    """The reference's BABYVLLM_PREFILL_ATTN switch (tests/test_paged_prefill.py:110-130 of
+    the reference): "triton" (the default) and "hip" run the HIP prefill kernel; "torch",
+    the reference's SDPA loop, is not part of this build and raises instead of falling back."""
+    import babyvllm.layers.attention as attn_mod
+    import babyvllm.kernels.paged_prefill as pp
+    from babyvllm.layers.attention import Attention
+    from babyvllm.worker.context import set_forward_context
+
+    assert attn_mod._PREFILL_BACKEND == "triton"
+    hkv, group, d = 4, 7, 128
+    q, kv_cache, md = build_prefill_case([(32, 9), (0, 20)], hkv, group, d)
+    attn = Attention(hkv * group, d, hkv)
+    attn.kv_cache = kv_cache
+    calls = []
+    real = pp.paged_prefill_attention
+    monkeypatch.setattr(pp, "paged_prefill_attention", lambda *a: calls.append(1) or real(*a))
+    for backend in ("triton", "hip"):
+        monkeypatch.setattr(attn_mod, "_PREFILL_BACKEND", backend)
+        with set_forward_context(md):
+            out = attn(q, q, q)
+        assert_attn_close(out, _oracle(q, kv_cache, md, group))
+    assert calls == [1, 1]
+    monkeypatch.setattr(attn_mod, "_PREFILL_BACKEND", "torch")
+    with set_forward_context(md), pytest.raises(RuntimeError, match="BABYVLLM_PREFILL_ATTN"):
+        attn(q, q, q)
+    assert calls == [1, 1]
+
+
 def test_empty_step_returns_empty():
     q, kv_cache, md = build_prefill_case([(0, 3)], 4, 7, 128)
     out = _kernel()(q[:0], kv_cache, md, 0.1)
