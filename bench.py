@@ -28,7 +28,9 @@ end-to-end generate of config 5. The host CPU (lscpu model, sockets, cores,
 threads) is recorded once in `cpu_host`.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
-                       [--only NAME] [--calib-copy]
+                       [--only NAME] [--calib-copy] [--tune KNOB=VALUE ...]
+(--tune sets a library tuning knob, bvllm_set_tuning, before measuring: for A/B
+runs and the profiles of the alternative kernels.)
 """
 
 from __future__ import annotations
