@@ -176,7 +176,8 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeArgs a) {
     if (ch == 0) red[q] = chain_max(r);
     __syncthreads();
     M = kNegInf;
-    for (int k = 0; k < NQ; ++k) M = fmaxf(M, red[k]);
+    const int nq = (np + kChain - 1) / kChain;  // chains holding results; the others' maxima are -inf
+    for (int k = 0; k < nq; ++k) M = fmaxf(M, red[k]);
   } else {
     M = kNegInf;
     for (int s = threadIdx.x; s < np; s += 256) M = fmaxf(M, lse[s]);
@@ -202,7 +203,11 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(DecodeArgs a) {
     if (ch == 0) gden[q] = den;
     __syncthreads();
     if (q == 0) {
-      for (int k = 0; k < NQ; ++k) {
+      // Chains past the set's last result have den == 0 and would be skipped
+      // below anyway; not visiting them saves a dependent LDS read each
+      // (B1 x 32768, 4 of 32 chains used: 25.7-26.4 -> 24.8-25.4 us).
+      const int nq = min(NQ, (np - set0 + kChain - 1) / kChain);
+      for (int k = 0; k < nq; ++k) {
         if (gden[k] == 0.f) continue;
         const float4 g = gnum[k][ch];
         if (!any) {
