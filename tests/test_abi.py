@@ -3,7 +3,6 @@ header declares with the argument counts the binding uses, rejects bad
 arguments on the host, and the Python layer never falls back to a non-HIP path.
 """
 
-import ctypes
 import os
 import re
 import subprocess
