@@ -20,14 +20,14 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
   decode_work_group<D, NW, PF>(a, blockIdx.x, smem);
 }
 
-// Two waves per split (PAIR), four pages in flight each.
-template <int D, bool NT>
+// Two waves per split, or per group of splits (PAIR), four pages in flight each.
+template <int D, bool NT, bool GROUP>
 __global__ __launch_bounds__(128) void paged_decode_pair_kernel(DecodeArgs a, int items) {
   __shared__ __attribute__((aligned(16))) unsigned char tile[2 * kTileBytes<D>];
-  __shared__ __attribute__((aligned(16))) float xs[kPairLdsFloats<D>];
+  __shared__ __attribute__((aligned(16))) float xs[(GROUP ? 2 : 1) * kPairLdsFloats<D>];
   const int item = (int)blockIdx.x;
   if (item >= items) return;
-  decode_stream_wave<D, 4, NT, false, true>(a, item, tile + wave_id() * kTileBytes<D>, xs);
+  decode_stream_wave<D, 4, NT, GROUP, true>(a, item, tile + wave_id() * kTileBytes<D>, xs);
 }
 
 // One streaming wave per work-group, so that a short batch's splits spread
@@ -266,11 +266,17 @@ DecodePlan decode_plan(int32_t batch, int32_t num_kv_heads, int32_t num_splits, 
   bool group_mode = p.group > 1 && (num_splits > kChain || (int64_t)batch * num_kv_heads * groups >= 512);
   const int forced = tuning(kTuneDecodeSplitMode);
   if (forced == 1 && (p.group == 1 || num_splits <= kChain)) group_mode = false;
-  if (forced == 2 && p.group > 1) group_mode = true;
+  if ((forced == 2 || forced == 3) && p.group > 1) group_mode = true;
   p.splits_per_item = group_mode ? p.group : 1;
   p.partials = group_mode ? (int32_t)groups : num_splits;
   p.fold_in_reduce = !group_mode && p.group > 1;
-  p.pair = !group_mode && forced != 1;
+  // Two waves per work-group: for single splits unless knob 1; for groups of
+  // splits when the one-wave grid has at most one wave per CU, since the
+  // two-wave group kernel runs one wave per SIMD (2 x 8192 and 4 x 4096, 256
+  // groups: 22.3-22.6 -> 19.7-20.3 us; 1 x 32768, 512 groups: 25.6-25.9 against
+  // 25.2-25.4 us on one wave; 8 x 32768: 116-119 against 106 us).
+  const int64_t group_items = (int64_t)batch * num_kv_heads * groups;
+  p.pair = group_mode ? (forced == 3 || (forced != 2 && group_items <= device_cus())) : forced != 1;
   return p;
 }
 
@@ -370,14 +376,17 @@ static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
   const int64_t items = (int64_t)a.batch * a.num_kv_heads * units;
   if (items > 0x7ffffff0) return hipErrorInvalidValue;
   hipError_t err;
-  if (a.splits_per_item > 1) {
-    err = launch_stream<D, true>(a, items, stream);
-  } else if (p.pair) {
-    if (tuning(kTuneDecodeCached) == 0)
-      hipLaunchKernelGGL((paged_decode_pair_kernel<D, true>), dim3((unsigned)items), dim3(128), 0, stream, a, (int)items);
-    else
-      hipLaunchKernelGGL((paged_decode_pair_kernel<D, false>), dim3((unsigned)items), dim3(128), 0, stream, a, (int)items);
+  if (p.pair) {
+    const bool group = a.splits_per_item > 1;
+    const bool nt = tuning(kTuneDecodeCached) == 0;
+    const dim3 grid((unsigned)items), block(128);
+    if (group && nt) hipLaunchKernelGGL((paged_decode_pair_kernel<D, true, true>), grid, block, 0, stream, a, (int)items);
+    else if (group) hipLaunchKernelGGL((paged_decode_pair_kernel<D, false, true>), grid, block, 0, stream, a, (int)items);
+    else if (nt) hipLaunchKernelGGL((paged_decode_pair_kernel<D, true, false>), grid, block, 0, stream, a, (int)items);
+    else hipLaunchKernelGGL((paged_decode_pair_kernel<D, false, false>), grid, block, 0, stream, a, (int)items);
     err = hipGetLastError();
+  } else if (a.splits_per_item > 1) {
+    err = launch_stream<D, true>(a, items, stream);
   } else {
     err = launch_stream<D, false>(a, items, stream);
   }

@@ -75,9 +75,10 @@ __device__ __forceinline__ float group_lse(const GroupFold& f) { return f.L > 0.
 // consecutive splits); `tile` is the wave's K transpose tile (kTileBytes<D>
 // bytes of LDS).
 // PAIR: the item's work-group has two waves; wave w holds states 2w and 2w+1
-// of the split (its pages 4k + 2w and 4k + 2w + 1), with four pages in flight
+// of each split (its pages 4k + 2w and 4k + 2w + 1), with four pages in flight
 // instead of two, and hands its states to wave 0 through `xs` (kPairLdsFloats<D>
-// floats of LDS), which merges the four in order as a single wave would.
+// floats of LDS, twice that with GROUP) at the end of every split; wave 0
+// merges the four in order as a single wave would.
 template <int D>
 constexpr int kPairLdsFloats = 2 * (2 + 4 * (D / 16)) * 64;
 
@@ -87,7 +88,7 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
   constexpr int KC = D / 32;
   constexpr int VD = D / 16;
   constexpr int OPL = D / 4;  // output floats per lane: head n, dims VD·(4g+i) + c
-  static_assert((!PAIR && PF == 2) || (PAIR && PF == 4 && !GROUP), "pages in flight per wave");
+  static_assert((!PAIR && PF == 2) || (PAIR && PF == 4), "pages in flight per wave");
   const int w = PAIR ? wave_id() : 0;
 
   const int G = a.num_heads / a.num_kv_heads;
@@ -225,6 +226,37 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
     reset();
   };
 
+  // PAIR: wave 1's states become states 2 and 3 of wave 0, through LDS
+  // buffer xb (one barrier; both waves call it). Wave 1's states restart.
+  auto pair_exchange = [&](int xb) __attribute__((always_inline)) {
+    float* xbase = xs + xb * kPairLdsFloats<D>;
+    if (w == 1) {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        float* rec = xbase + s2 * (2 + 4 * VD) * 64;
+        rec[lane] = st[s2].m;
+        rec[64 + lane] = st[s2].l;
+#pragma unroll
+        for (int c = 0; c < VD; ++c) *reinterpret_cast<f32x4_t*>(rec + 128 + (c * 64 + lane) * 4) = st[s2].acc[c];
+      }
+      reset();
+    }
+    __syncthreads();
+    if (w == 0) {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const float* rec = xbase + s2 * (2 + 4 * VD) * 64;
+        st[2 + s2].m = rec[lane];
+        st[2 + s2].l = rec[64 + lane];
+#pragma unroll
+        for (int c = 0; c < VD; ++c)
+          st[2 + s2].acc[c] = *reinterpret_cast<const f32x4_t*>(rec + 128 + (c * 64 + lane) * 4);
+      }
+    }
+  };
+  int xb = 0;  // PAIR with GROUP: the exchange buffers alternate, so wave 1 never
+               // overwrites a record wave 0 has not read (a barrier lies between)
+
   int cur = j0;  // split whose states are open
   // Item-relative page index where split cur + 1 starts (none past the unit).
   int next_start = (cur + 1 < j1) ? bps : INT_MAX;
@@ -251,14 +283,25 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
       for (int k = 0; k < here; k += 8) {
 #pragma unroll
         for (int i = 0; i < PF; ++i) {
+          const int quad = k + 4 * (i >> 1);  // first page of the 4-page block of slot i
+          if constexpr (GROUP) {
+            if ((i & 1) == 0 && quad < here && base + quad == next_start) {  // a new split starts here
+              pair_exchange(xb);
+              xb ^= 1;
+              if (w == 0) finish_split(cur);
+              ++cur;
+              next_start = (cur + 1 < j1) ? next_start + bps : INT_MAX;
+              any = false;
+            }
+          }
           wait_page<(PF - 1) * kLoadsPerPage, D>(r[i]);
-          const int q = k + 4 * (i >> 1) + 2 * w + (i & 1);
+          const int q = quad + 2 * w + (i & 1);
           if (q < here)
             process_page<D>(st[i & 1], r[i], qb, tile, n, g, (p0 + base + q) * 16 + 4 * g, seq_len, a.scale_log2);
           const int64_t pn = phys(min(q + 8, here - 1)) * a.c_sb;
           load_page<D, NT>(r[i], kc + pn, vc + pn, off);
+          if ((i & 1) == 1 && quad < here) any = true;
         }
-        any = true;
       }
 #pragma unroll
       for (int i = 0; i < PF; ++i) wait_page<0, D>(r[i]);
@@ -295,27 +338,10 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
     for (int i = 0; i < PF; ++i) wait_page<0, D>(r[i]);
   }
   if constexpr (PAIR) {
-    // Wave 1's states become states 2 and 3 of wave 0.
-    if (w == 1) {
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        float* rec = xs + s2 * (2 + 4 * VD) * 64;
-        rec[lane] = st[s2].m;
-        rec[64 + lane] = st[s2].l;
-#pragma unroll
-        for (int c = 0; c < VD; ++c) *reinterpret_cast<f32x4_t*>(rec + 128 + (c * 64 + lane) * 4) = st[s2].acc[c];
-      }
-    }
-    __syncthreads();
+    // The last split's states (both waves agree on `any`: it follows the
+    // 4-page blocks, not the pages each wave computed).
+    if (any || !GROUP) pair_exchange(xb);
     if (w == 1) return;
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      const float* rec = xs + s2 * (2 + 4 * VD) * 64;
-      st[2 + s2].m = rec[lane];
-      st[2 + s2].l = rec[64 + lane];
-#pragma unroll
-      for (int c = 0; c < VD; ++c) st[2 + s2].acc[c] = *reinterpret_cast<const f32x4_t*>(rec + 128 + (c * 64 + lane) * 4);
-    }
   }
   // The split holding the unit's last pages (for a unit of one split, also
   // when it has no page: its partial is written as empty).

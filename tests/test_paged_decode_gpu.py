@@ -208,14 +208,14 @@ def test_reduce_bits_do_not_depend_on_the_split_count(n, monkeypatch):
 
 def _modes(q, kv_cache, bt, seq_lens, scale, bucket, partition):
     """Outputs of every launch choice that must give the same bits: split mode
-    (two waves per split by default, one wave per split, one wave per group of
-    4 splits), wave order, nontemporal page loads, single pass on streaming
-    waves."""
+    (two waves per split by default, one wave per split, one or two waves per
+    group of 4 splits), wave order, nontemporal page loads, single pass on
+    streaming waves."""
     from babyvllm.kernels import _lib
 
     outs = {}
     choices = [("auto", None, 0), ("per_split", _lib.TUNE_DECODE_SPLIT_MODE, 1),
-               ("per_group", _lib.TUNE_DECODE_SPLIT_MODE, 2),
+               ("per_group", _lib.TUNE_DECODE_SPLIT_MODE, 2), ("pair_group", _lib.TUNE_DECODE_SPLIT_MODE, 3),
                ("order1", _lib.TUNE_DECODE_ORDER, 1), ("cached", _lib.TUNE_DECODE_CACHED, 1),
                ("stream_single", _lib.TUNE_DECODE_SINGLE_PASS_STREAM, 1)]
     for name, knob, value in choices:
@@ -232,9 +232,10 @@ def _modes(q, kv_cache, bt, seq_lens, scale, bucket, partition):
 @pytest.mark.parametrize("lens", [[600, 37, 0, 1], [2047, 16, 64, 300], [5000, 129], [130, 129, 128, 127]])
 def test_launch_choices_do_not_change_bits(partition, lens, monkeypatch):
     """Every launch choice of one plan gives identical bits: two waves or one
-    wave per split (groups of 4 splits folded in the reduce) or one per group
-    (folded in the wave), either wave order, with or without the nontemporal
-    hint, and the single pass on work-groups or streaming waves.
+    wave per split (groups of 4 splits folded in the reduce) or one or two per
+    group (folded in the wave, the two waves handing states over at every
+    split's end), either wave order, with or without the nontemporal hint, and
+    the single pass on work-groups or streaming waves.
     Rows longer than the bucket and rows ending inside a group are covered."""
     from babyvllm.kernels.decode_split import DECODE_PARTITION_ENV
 
