@@ -304,6 +304,26 @@ def test_random_ragged_batches(seed):
             assert actual[row].abs().max() == 0
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_random_batches_launch_choices_agree(seed):
+    """Seeded random batches (1-16 rows of 0-5000 tokens, buckets up to 4096
+    tokens past the longest row, partitions from 1 page to auto): every launch
+    choice of the plan gives the same bits, including the split-mode and
+    group-mode kernels on one or two waves."""
+    g = torch.Generator().manual_seed(5000 + seed)
+    hkv, group, d = _HEAD_CONFIGS[int(torch.randint(len(_HEAD_CONFIGS), (1,), generator=g))]
+    B = int(torch.randint(1, 17, (1,), generator=g))
+    lens = [0 if int(torch.randint(8, (1,), generator=g)) == 0 else int(torch.randint(1, 5001, (1,), generator=g))
+            for _ in range(B)]
+    bucket = max(max(lens), 1) + int(torch.randint(0, 4097, (1,), generator=g))
+    partition = [None, 1, 2, 4, 8, 16][int(torch.randint(6, (1,), generator=g))]
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, hkv=hkv, group=group, d=d,
+                                                   width=cdiv(bucket, BLOCK_SIZE) + 1, seed=seed)
+    outs = _modes(q, kv_cache, bt, seq_lens, d ** -0.5, bucket, partition)
+    for name, out in outs.items():
+        assert torch.equal(out, outs["auto"]), name
+
+
 # ------------------------------------------- reduce over more than one set of groups
 
 def test_more_splits_than_one_reduce_set():
