@@ -14,8 +14,6 @@ import torch
 
 from babyvllm.kernels import _lib
 
-MAX_FUSED_SIZE = 65536
-
 
 def fused_add_rms_norm(input: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor, eps: float):
     original_shape = input.shape
@@ -28,8 +26,6 @@ def fused_add_rms_norm(input: torch.Tensor, residual: torch.Tensor | None, weigh
         residual_2d = residual.view(-1, residual.shape[-1])
         assert residual_2d.stride(-1) == 1, "Residual last dimension must be contiguous"
     M, N = input_2d.shape
-    if N > MAX_FUSED_SIZE:
-        raise RuntimeError(f"Hidden size {N} too large for fused RMSNorm")
     for name, t in (("input", input_2d), ("weight", weight)):
         _lib.require_rocm_tensor(name, t)
     if input.dtype != torch.bfloat16:

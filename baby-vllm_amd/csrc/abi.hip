@@ -124,7 +124,8 @@ extern "C" int bvllm_paged_decode(const void* q, int64_t q_stride_b, int64_t q_s
   a.scale_log2 = scale * kLog2e;
   a.out = out; a.o_sb = out_stride_b; a.o_sh = out_stride_h;
   if (ws_bytes > 0) {
-    const int64_t rows = ws_bytes / (int64_t)((head_dim + 1) * sizeof(float));
+    a.ws_partials = decode_partials(batch, num_kv_heads, num_splits, blocks_per_split);
+    const int64_t rows = (int64_t)batch * num_heads * a.ws_partials;
     a.part_out = reinterpret_cast<float*>(workspace);
     a.part_lse = a.part_out + rows * head_dim;
   }

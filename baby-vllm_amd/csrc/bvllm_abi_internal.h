@@ -38,7 +38,8 @@ struct DecodeArgs {
   int32_t waves;                           // waves per single-pass work-group (4; 0 = default)
   // Set by the launcher for split launches (decode_plan):
   int32_t splits_per_item;                 // consecutive splits one streaming wave computes
-  int32_t num_partials;                    // partial states per (row, head) in the workspace
+  int32_t num_partials;                    // partial states per (row, head) the launch writes
+  int32_t ws_partials;                     // partial states per (row, head) the workspace holds
   int32_t item_order;                      // 0: KV head fastest in the wave numbering; 1: split unit fastest
   // Prefill view (both null for a decode batch): row b is sequence b of a
   // varlen prefill batch. Only sequences with exactly one query token are
@@ -111,7 +112,8 @@ struct DecodePlan {
   bool pair;               // one split or group per work-group of two waves (two states each)
 };
 DecodePlan decode_plan(int32_t batch, int32_t num_kv_heads, int32_t num_splits, int32_t blocks_per_split);
-// Partial states (per row and head) one decode launch writes to the workspace.
+// Partial states per (row, head) the decode workspace holds: the most any
+// plan of these splits writes, independent of the tuning knobs.
 int32_t decode_partials(int32_t batch, int32_t num_kv_heads, int32_t num_splits, int32_t blocks_per_split);
 
 // Process-wide tuning switches (bvllm_set_tuning). Knob values: 0 = default.

@@ -280,8 +280,17 @@ DecodePlan decode_plan(int32_t batch, int32_t num_kv_heads, int32_t num_splits, 
   return p;
 }
 
+// The largest partial count any plan of these splits can write, whatever the
+// split-mode knob says: groups only where split mode is impossible (more than
+// kChain splits that group), else one per split. It sizes the workspace and
+// places part_lse, so a knob changed between the size query and the launch
+// cannot move either.
 int32_t decode_partials(int32_t batch, int32_t num_kv_heads, int32_t num_splits, int32_t blocks_per_split) {
-  return decode_plan(batch, num_kv_heads, num_splits, blocks_per_split).partials;
+  (void)batch;
+  (void)num_kv_heads;
+  if (num_splits <= 1) return 0;
+  if (blocks_per_split % kSplitGroup == 0 && num_splits > kChain) return (num_splits + kSplitGroup - 1) / kSplitGroup;
+  return num_splits;
 }
 
 template <int D>
@@ -372,6 +381,9 @@ static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
   }
   a.splits_per_item = p.single_pass ? 1 : p.splits_per_item;
   a.num_partials = p.partials;
+  // The workspace holds decode_partials() states per (row, head); the plan
+  // (one knob read above) never asks for more.
+  if (!p.single_pass && (a.part_out == nullptr || p.partials > a.ws_partials)) return hipErrorInvalidValue;
   const int64_t units = (a.num_splits + a.splits_per_item - 1) / a.splits_per_item;
   const int64_t items = (int64_t)a.batch * a.num_kv_heads * units;
   if (items > 0x7ffffff0) return hipErrorInvalidValue;

@@ -78,10 +78,10 @@ def build_decode(batch, ctx, layers, seed=0):
         bt = torch.zeros(batch, width, dtype=torch.int32, device="cuda")
         bt[:, :blocks] = torch.randperm(total, device="cuda", generator=g).view(batch, blocks).to(torch.int32)
         tables.append(bt)
-    # N(0,1) q; the 1/sqrt(128) enters as the softmax scale, as Attention passes it.
-    q = torch.randn(batch, H, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    # N(0,1) q, one per layer; the 1/sqrt(128) enters as the softmax scale, as Attention passes it.
+    qs = [torch.randn(batch, H, D, device="cuda", dtype=torch.bfloat16, generator=g) for _ in range(layers)]
     seq_lens = torch.full((batch,), ctx, dtype=torch.int32, device="cuda")
-    return q, caches, tables, seq_lens
+    return qs, caches, tables, seq_lens
 
 
 def time_graph(fn, warmup, iters):
@@ -118,18 +118,19 @@ def bench_decode(batch, ctx, warmup, iters, layers=LAYERS):
     from babyvllm.kernels.decode_split import decode_split_plan
     from babyvllm.kernels.paged_attn import _num_sms, paged_decode_attention
 
-    q, caches, tables, seq_lens = build_decode(batch, ctx, layers, seed=batch + ctx)
+    qs, caches, tables, seq_lens = build_decode(batch, ctx, layers, seed=batch + ctx)
     scale = D ** -0.5
+    outs = []  # every layer's output stays allocated in the graph's pool (no reuse across layers)
 
     def fwd():
-        for i in range(layers):
-            paged_decode_attention(q, caches[i], tables[i], seq_lens, scale, max_seq_len=ctx)
+        outs[:] = [paged_decode_attention(qs[i], caches[i], tables[i], seq_lens, scale, max_seq_len=ctx)
+                   for i in range(layers)]
 
     ms, _ = time_graph(fwd, warmup, iters)
     kv_bytes = batch * ctx * HKV * D * 2 * 2
     per_launch_us = ms * 1e3 / layers
     plan = decode_split_plan(batch, HKV, BS, tables[0].shape[1], ctx, _num_sms(0))
-    del q, caches, tables, seq_lens
+    del qs, caches, tables, seq_lens, outs
     torch.cuda.empty_cache()
     return {
         "batch": batch, "context": ctx, "plan": list(plan),
@@ -256,16 +257,19 @@ def bench_prefill(name, warmup, iters, layers=LAYERS):
             context_lens=torch.tensor([c for c, _ in specs], dtype=torch.int32, device="cuda"),
             query_start_loc_cpu=qsl, seq_lens_cpu=seq_lens, context_lens_cpu=[c for c, _ in specs],
             max_query_len=max(q_lens), max_seq_len=max(seq_lens)))
-    q = torch.randn(sum(q_lens), H, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    # Every layer reads its own q and writes its own output, and all 28 outputs
+    # stay allocated in the graph's pool, so no layer finds its q or output
+    # lines in the 256 MB Infinity Cache from the previous layer.
+    qs = [torch.randn(sum(q_lens), H, D, device="cuda", dtype=torch.bfloat16, generator=g) for _ in range(layers)]
+    outs = []
 
     def fwd():
-        for i in range(layers):
-            paged_prefill_attention(q, caches[i], mds[i], D ** -0.5)
+        outs[:] = [paged_prefill_attention(qs[i], caches[i], mds[i], D ** -0.5) for i in range(layers)]
 
     ms, _ = time_graph(fwd, warmup, iters)
     per_us = ms * 1e3 / layers
     flops = prefill_flops(specs)
-    del caches, mds, q
+    del caches, mds, qs, outs
     torch.cuda.empty_cache()
     return {"us_per_layer": per_us, "tflop_s": flops / (per_us * 1e-6) / 1e12, "flop": flops,
             "roofline": binding_roof(flops, prefill_bytes(specs), per_us * 1e-6)}
@@ -275,11 +279,13 @@ def bench_prefill(name, warmup, iters, layers=LAYERS):
 C1_H, C1_HKV, C1_D, C1_B, C1_POOL, C1_WIDTH, C1_BUCKET = 14, 2, 64, 8, 512, 32, 512
 
 
-def config1_inputs(seed, device):
-    """Lengths U[100, 512], a 512-block pool whose rows are a seeded permutation
-    (width 32), q/k/v ~ N(0, 1); the step's token sits at position seq_len - 1."""
+def config1_inputs(seed, device, lens=None):
+    """Lengths U[100, 512] (or the given ones), a 512-block pool whose rows are a
+    seeded permutation (width 32), q/k/v ~ N(0, 1); the step's token sits at
+    position seq_len - 1."""
     g = torch.Generator().manual_seed(seed)
-    lens = torch.randint(100, 513, (C1_B,), generator=g)
+    drawn = torch.randint(100, 513, (C1_B,), generator=g)
+    lens = drawn if lens is None else lens
     cache = torch.randn(2, C1_POOL, BS, C1_HKV, C1_D, generator=g)
     bt = torch.randperm(C1_POOL, generator=g)[: C1_B * C1_WIDTH].view(C1_B, C1_WIDTH).int()
     qkv = torch.randn(C1_B, (C1_H + 2 * C1_HKV) * C1_D, generator=g)
@@ -297,15 +303,22 @@ def config1_bytes(lens):
 
 def bench_config1(warmup, iters, layers=24):
     """One 'step' = the config-1 step for each of the 0.5B model's 24 layers, each
-    layer on its own 512-block pool: RoPE (theta 1e6) + append through
-    slot_mapping, then paged decode with max_seq_len = 512."""
+    layer on its own 512-block pool, table and q/k/v: RoPE (theta 1e6) + append
+    through slot_mapping, then paged decode with max_seq_len = 512. As in the
+    model, every layer of the step sees the same lengths and positions (seed
+    100's); each layer's slots follow from those positions and its own table."""
     from babyvllm.kernels.paged_attn import paged_decode_attention
     from babyvllm.kernels.rope import fused_rope_and_cache
     from babyvllm.layers.rotary import RotaryEmbedding
 
-    per_layer = [config1_inputs(100 + i, "cuda") for i in range(layers)]
-    lens, _, _, _, pos, _ = per_layer[0]
-    seq_lens = lens.int()
+    lens = config1_inputs(100, "cpu")[0]
+    per_layer = [config1_inputs(100 + i, "cuda", lens=lens) for i in range(layers)]
+    pos = per_layer[0][4]
+    seq_lens = lens.int().cuda()
+    for _, _, bt, _, p, slots in per_layer:
+        bt, p = bt.cpu(), p.cpu()
+        assert torch.equal(p, pos.cpu())
+        assert torch.equal(slots.cpu(), bt[torch.arange(C1_B), p // BS].long() * BS + p % BS)
     rope = RotaryEmbedding(C1_D, 4096, base=1e6).cuda()
     views = []
     for _, cache, bt, qkv, _, slots in per_layer:
@@ -322,7 +335,7 @@ def bench_config1(warmup, iters, layers=24):
 
     ms, _ = time_graph(fwd, warmup, iters)
     per_us = ms * 1e3 / layers
-    nbytes = config1_bytes(lens.cpu())
+    nbytes = config1_bytes(lens)
     del per_layer, views
     torch.cuda.empty_cache()
     return {"us_per_layer": per_us, "gb_s": nbytes / (per_us * 1e-6) / 1e9, "algorithmic_bytes": nbytes,
@@ -490,6 +503,64 @@ def cpu_time(fn, budget_s=10.0, min_runs=5, max_runs=50):
 def _cpu_line(value, unit, sec, runs, sample):
     return {"value": round(value, 4), "unit": unit, "cores": cpu_threads(), "kind": "port",
             "ms": round(sec * 1e3, 3), "runs": runs, "sample": sample}
+
+
+# What the compact secondary entries of the JSON line mean (stated once).
+LEGEND = {
+    "us": "time per call: median replay of a hipGraph of 28 calls (24 for config 1), each call on its own "
+          "cache pool, q and output, divided by the calls",
+    "ach/unit": "algorithmic work per call / us; work = bytes for bound hbm, flop for bound mfma",
+    "frac": "ach / the bound's peak (hbm 8000 GB/s, mfma 2500 TFLOP/s dense bf16)",
+    "cpu": "the oracle's fp32 restatement of the reference's torch CPU path on one call of the same shape "
+           "(gather + SDPA decode, per-sequence SDPA prefill loop, apply_rope + index_copy_ append, torch "
+           "argmax / add + RMSNorm / SiLU*mul), median of >= 5 runs after a warm-up on cpu_host.threads_used "
+           "threads: [ms, value in the line's unit]",
+}
+
+
+def compact(r):
+    """A secondary line as it goes into the JSON line (full figures go to stderr)."""
+    roof = r.get("roofline") or {}
+    us = r.get("us_per_layer", r.get("us_per_call"))
+    out = {"us": round(us, 2), "ach": roof.get("achieved"), "unit": roof.get("unit"), "frac": roof.get("frac"),
+           "bound": roof.get("bound"),
+           "work": roof.get("flop") if roof.get("bound") == "mfma" else roof.get("algorithmic_bytes")}
+    if "plan" in r:
+        out["plan"] = r["plan"]
+    if "roof_us" in roof:
+        out["roof_us"] = roof["roof_us"]
+    cpu = r.get("cpu_baseline")
+    if cpu and cpu.get("value") is not None:
+        out["cpu"] = [cpu["ms"], cpu["value"]]
+    return out
+
+
+def compact_generate(r):
+    return {"tok_s": round(r["tokens_per_s"], 1), "wall_s": round(r["wall_s"], 3),
+            "ttft_ms": [round(r["ttft_mean_ms"], 1), round(r["ttft_max_ms"], 1)],
+            "kv_peak": r["kv_blocks_peak"], "kv_closed_form": r["kv_blocks_closed_form_all_at_once"],
+            "hit_tokens": r["prefix_hit_tokens"], "steps": r["engine_steps"], "cpu": None}
+
+
+def summary_table(head, secondary, host):
+    """The per-config figures as the last lines of stderr."""
+    rows = [("decode_b64_ctx1920 (headline)", compact(head))]
+    rows += [(k, compact(v)) for k, v in secondary.items() if "roofline" in v]
+    log("")
+    log(f"{'config':<36} {'us':>9} {'achieved':>10} {'unit':>8} {'frac':>7} {'bound':>5} {'cpu ms':>10} "
+        f"{'cpu value':>10}")
+    for name, c in rows:
+        cpu = c.get("cpu") or ["-", "-"]
+        log(f"{name:<36} {c['us']:>9} {c['ach']:>10} {c['unit']:>8} {c['frac']:>7} {c['bound']:>5} "
+            f"{cpu[0]:>10} {cpu[1]:>10}")
+    for k, v in secondary.items():
+        if k.startswith("generate"):
+            g = compact_generate(v)
+            log(f"{k:<36} {g['tok_s']} new tok/s, wall {g['wall_s']} s, TTFT mean/max {g['ttft_ms']} ms, "
+                f"KV peak {g['kv_peak']} pages (closed form {g['kv_closed_form']}), {g['hit_tokens']} hit tokens")
+    if host:
+        log(f"cpu baseline host: {host.get('model')}, {host.get('physical_cores')} cores, "
+            f"{host['threads_used']} threads used")
 
 
 def cpu_decode(batch, ctx, budget_s=10.0):
@@ -758,13 +829,6 @@ def main():
             secondary[key]["cpu_baseline"] = {
                 "value": None, "note": "not timed: the reference's torch path on the CPU would take minutes per "
                                        "generated token of the 28-layer 7B model at 64 x 1920"}
-        secondary["reference_h100_published"] = {
-            "decode_b64_ctx2048_gb_s": 2514.9, "prefill_1x(2048+4096)_ms": 1.2615,
-            "generate_b64_distinct_caching_off_tok_s": 1135.96, "generate_ttft_ms": 2902.94,
-            "source": "results_28Oct2026_H100_flash_decode/decode_attn_bench.json:1200-1208; "
-                      "results_28Oct2026_H100_flash_decode/comparison_baby_partition_auto.json:705-707; "
-                      "results_26Oct2026_H100/prefill_attn_bench_torch2.13.json:43-46",
-        }
 
     cpu = None
     host = None
@@ -807,9 +871,17 @@ def main():
             "launch_us": round(head["us_per_layer"], 3),
         },
         "cpu_baseline": cpu,
-        "cpu_host": host,
-        "secondary": secondary,
+        "cpu_host": None if host is None else {k: host.get(k) for k in ("model", "physical_cores",
+                                                                         "threads_used")},
     }
+    if secondary:
+        line["secondary"] = {k: (compact_generate(v) if k.startswith("generate") else compact(v))
+                             for k, v in secondary.items()}
+        line["legend"] = LEGEND
+        line["reference_h100"] = {"decode_b64_ctx2048_gb_s": 2514.9, "prefill_1x(2048+4096)_ms": 1.2615,
+                                  "generate_b64_distinct_tok_s": 1135.96}
+    log("full secondary figures: " + json.dumps(secondary))
+    summary_table(head, secondary, host)
     print(json.dumps(line), flush=True)
 
 

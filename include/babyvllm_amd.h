@@ -77,8 +77,11 @@ BVLLM_API int bvllm_rope_kv_append(void* q, int64_t q_stride_t, int64_t q_stride
  * Bytes of device scratch bvllm_paged_decode needs for one launch (0 = none):
  * fp32 partial outputs [B, H, P, D] and log-sum-exps [B, H, P], the
  * reference's part_out / part_lse (babyvllm/kernels/paged_attn.py:317-318),
- * where P is the number of splits, or of groups of 4 consecutive splits when
- * the launch folds each group before writing it (plans with many splits).
+ * where P is the number of splits, or, for plans of more than 32 splits whose
+ * pages per split are a multiple of 4, the number of groups of 4 consecutive
+ * splits (those launches fold each group before writing it). The size and
+ * layout depend only on these arguments, never on bvllm_set_tuning: knob 0
+ * may make a launch write fewer partials than P, never more.
  */
 BVLLM_API int64_t bvllm_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                                                int32_t head_dim, int32_t num_splits,

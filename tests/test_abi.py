@@ -67,6 +67,27 @@ def test_workspace_bytes_formula():
     assert h.bvllm_decode_workspace_bytes(8, 28, 4, 128, 15, 8) == 8 * 28 * 15 * (128 + 1) * 4
     # Single pass: no scratch.
     assert h.bvllm_decode_workspace_bytes(64, 28, 4, 128, 1, 120) == 0
+    # B1 x 32768: 512 splits of 4 pages fold into 128 groups of 4 splits.
+    assert h.bvllm_decode_workspace_bytes(1, 28, 4, 128, 512, 4) == 28 * 128 * 129 * 4
+    # 512 splits of 6 pages cannot fold: one partial per split.
+    assert h.bvllm_decode_workspace_bytes(1, 28, 4, 128, 512, 6) == 28 * 512 * 129 * 4
+
+
+def test_workspace_bytes_ignore_the_split_mode_knob():
+    # The size (and the place of part_lse inside it) must not follow knob 0:
+    # a knob changed between the size query and the launch would otherwise make
+    # the kernels write past the workspace.
+    mod = _lib()
+    h = mod.lib()
+    plans = [(8, 15, 8), (64, 2, 60), (16, 8, 16), (1, 512, 4), (2, 40, 8), (4, 20, 4), (1, 7, 5)]
+    want = {p: h.bvllm_decode_workspace_bytes(p[0], 28, 4, 128, p[1], p[2]) for p in plans}
+    try:
+        for knob_value in (1, 2, 3):
+            mod.set_tuning(mod.TUNE_DECODE_SPLIT_MODE, knob_value)
+            for p in plans:
+                assert h.bvllm_decode_workspace_bytes(p[0], 28, 4, 128, p[1], p[2]) == want[p], (knob_value, p)
+    finally:
+        mod.set_tuning(mod.TUNE_DECODE_SPLIT_MODE, 0)
 
 
 def test_host_side_argument_rejection():
@@ -88,9 +109,10 @@ def test_host_side_argument_rejection():
     assert h.bvllm_paged_decode(None, 0, 0, None, None, 0, 0, 0, 0, None, 0, 0, None, 1.0,
                                 None, 0, 0, None, 1, 1, 1, 34, 2, 128, 16, 0, None) == bad
     assert b"invalid argument" in h.bvllm_error_string(bad)
-    # waves must be 0, 4 or 8
-    assert h.bvllm_paged_decode(None, 0, 0, None, None, 0, 0, 0, 0, None, 0, 0, None, 1.0,
-                                None, 0, 0, None, 1, 1, 1, 28, 4, 128, 16, 5, None) == bad
+    # waves must be 0 or 4 (8 was accepted by an earlier ABI and is refused now)
+    for waves in (5, 8):
+        assert h.bvllm_paged_decode(None, 0, 0, None, None, 0, 0, 0, 0, None, 0, 0, None, 1.0,
+                                    None, 0, 0, None, 1, 1, 1, 28, 4, 128, 16, waves, None) == bad
     # Nothing to do is a success that launches nothing.
     assert h.bvllm_paged_decode(None, 0, 0, None, None, 0, 0, 0, 0, None, 0, 0, None, 1.0,
                                 None, 0, 0, None, 1, 1, 0, 28, 4, 128, 16, 0, None) == 0

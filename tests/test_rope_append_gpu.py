@@ -249,11 +249,15 @@ def test_special_values_bitwise(layout):
     with tuned(5, layout):
         _kernel()(q, k, v, cos, sin, cache, slots)
         torch.cuda.synchronize()
-    for got, want in ((q, qr), (k, kr), (cache, cr)):
+    for got, want in ((q, qr), (k, kr), (cache[0], cr[0])):
         got, want = got.cpu(), want.cpu()
         nan = want.isnan()
         assert torch.equal(got.isnan(), nan)
         assert torch.equal(got[~nan].view(torch.int16), want[~nan].view(torch.int16))
+    # V rows are copied, not computed: every bit, NaN sign and payload included,
+    # and untouched slots stay zero.
+    assert torch.equal(cache[1].cpu().view(torch.int16), cr[1].view(torch.int16))
+    assert torch.equal(cache[1].view(-1, Hkv, D)[slots].cpu().view(torch.int16), v.cpu().view(torch.int16))
 
 
 @pytest.mark.parametrize("layout", _LAYOUTS)
