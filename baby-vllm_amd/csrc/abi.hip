@@ -13,9 +13,7 @@ constexpr int kBad = (int)hipErrorInvalidValue;
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-bool valid_heads(int32_t h, int32_t hkv) {
-  return h > 0 && hkv > 0 && h % hkv == 0 && h / hkv <= 16;
-}
+bool valid_heads(int32_t h, int32_t hkv) { return h > 0 && hkv > 0 && h % hkv == 0; }
 
 }  // namespace
 

@@ -112,6 +112,12 @@ struct DecodePlan {
   bool pair;               // one split or group per work-group of two waves (two states each)
 };
 DecodePlan decode_plan(int32_t batch, int32_t num_kv_heads, int32_t num_splits, int32_t blocks_per_split);
+// Column groups of a decode launch: its KV heads, each cut into ceil(G / 16)
+// groups of at most 16 query heads (one MFMA tile of columns) when G > 16.
+inline int64_t decode_col_groups(const DecodeArgs& a) {
+  const int G = a.num_heads / a.num_kv_heads;
+  return (int64_t)a.num_kv_heads * ((G + 15) / 16);
+}
 // Partial states per (row, head) the decode workspace holds: the most any
 // plan of these splits writes, independent of the tuning knobs.
 int32_t decode_partials(int32_t batch, int32_t num_kv_heads, int32_t num_splits, int32_t blocks_per_split);

@@ -374,7 +374,7 @@ static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
     static std::atomic<bool> done[64] = {};
     hipError_t err = allow_lds(&paged_decode_kernel<D, NW, 2>, done, 160 * 1024);
     if (err != hipSuccess) return err;
-    const int64_t wgs = (int64_t)a.batch * a.num_kv_heads;
+    const int64_t wgs = (int64_t)a.batch * decode_col_groups(a);
     if (wgs > 0x7fffffff) return hipErrorInvalidValue;
     hipLaunchKernelGGL((paged_decode_kernel<D, NW, 2>), dim3((unsigned)wgs), dim3(NW * 64), smem, stream, a);
     return hipGetLastError();
@@ -385,7 +385,7 @@ static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
   // (one knob read above) never asks for more.
   if (!p.single_pass && (a.part_out == nullptr || p.partials > a.ws_partials)) return hipErrorInvalidValue;
   const int64_t units = (a.num_splits + a.splits_per_item - 1) / a.splits_per_item;
-  const int64_t items = (int64_t)a.batch * a.num_kv_heads * units;
+  const int64_t items = (int64_t)a.batch * decode_col_groups(a) * units;
   if (items > 0x7ffffff0) return hipErrorInvalidValue;
   hipError_t err;
   if (p.pair) {

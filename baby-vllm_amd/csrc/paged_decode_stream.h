@@ -71,9 +71,10 @@ __device__ __forceinline__ float group_fold_value(float acc, float x, float wa, 
 __device__ __forceinline__ float group_inv(const GroupFold& f) { return f.L > 0.f ? 1.f / f.L : 0.f; }
 __device__ __forceinline__ float group_lse(const GroupFold& f) { return f.L > 0.f ? f.M + __log2f(f.L) : kNegInf; }
 
-// One streaming decode wave: item = (row, KV head, unit of a.splits_per_item
-// consecutive splits); `tile` is the wave's K transpose tile (kTileBytes<D>
-// bytes of LDS).
+// One streaming decode wave: item = (row, column group, unit of
+// a.splits_per_item consecutive splits), the column group being the KV head
+// when G <= 16 (ColGroup); `tile` is the wave's K transpose tile
+// (kTileBytes<D> bytes of LDS).
 // PAIR: the item's work-group has two waves; wave w holds states 2w and 2w+1
 // of each split (its pages 4k + 2w and 4k + 2w + 1), with four pages in flight
 // instead of two, and hands its states to wave 0 through `xs` (kPairLdsFloats<D>
@@ -91,22 +92,26 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
   static_assert((!PAIR && PF == 2) || (PAIR && PF == 4), "pages in flight per wave");
   const int w = PAIR ? wave_id() : 0;
 
-  const int G = a.num_heads / a.num_kv_heads;
   const int S = a.num_splits;
   const int spi = GROUP ? a.splits_per_item : 1;
   const int units = (S + spi - 1) / spi;
-  int kvh, unit, b;
+  // Column groups: the KV heads, or their 16-head parts when G > 16 (ColGroup).
+  const int ncg = a.num_kv_heads * col_groups_per_kv(a.num_heads / a.num_kv_heads);
+  int cg, unit, b;
   if (a.item_order == 0) {  // KV head fastest: the 4 head slices of a page are requested together
-    kvh = item % a.num_kv_heads;
-    const int rest = item / a.num_kv_heads;
+    cg = item % ncg;
+    const int rest = item / ncg;
     unit = rest % units;
     b = rest / units;
   } else {  // unit fastest
     unit = item % units;
     const int rest = item / units;
-    kvh = rest % a.num_kv_heads;
-    b = rest / a.num_kv_heads;
+    cg = rest % ncg;
+    b = rest / ncg;
   }
+  const ColGroup cgp = col_group(a.num_heads / a.num_kv_heads, cg);
+  const int G = cgp.cols;  // heads of this column group
+  const int kvh = cgp.kvh;
   const int j0 = unit * spi;
   const int j1 = min(j0 + spi, S);
   const int bps = a.blocks_per_split;
@@ -124,7 +129,7 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
   uint4 qb[KC];
   {
     const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_sb +
-                           (int64_t)(kvh * G + n) * a.q_sh;
+                           (int64_t)(cgp.head0 + n) * a.q_sh;
 #pragma unroll
     for (int c = 0; c < KC; ++c) qb[c] = (n < G) ? ld16(qrow + 8 * (4 * c + g)) : make_uint4(0, 0, 0, 0);
   }
@@ -158,7 +163,7 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
   for (int k = 0; k < (GROUP ? OPL : 1); ++k) go[k] = 0.f;
   GroupFold gf;
 
-  const int64_t head = (int64_t)kvh * G + n;
+  const int64_t head = (int64_t)cgp.head0 + n;
   // Merges the 4 states of split `split` (merge_states' arithmetic, per lane)
   // and folds or writes its (o, lse).
   auto finish_split = [&](int split) __attribute__((always_inline)) {

@@ -6,7 +6,8 @@
 // the single-pass decode; the page math (page_scores, page_softmax_pv) is
 // shared with the split launches.
 //
-// Work-group = (sequence b, KV head) of a single-pass launch. Its NW = 4 waves
+// Work-group = (sequence b, KV head) of a single-pass launch (with more than 16
+// query heads per KV head, (sequence b, column group): see ColGroup). Its NW = 4 waves
 // walk the row's pages interleaved (wave w takes pages w, w+4, ...), each with
 // a private online-softmax state, and merge the 4 states in LDS in wave order.
 // The split launches (paged_decode_stream.h) keep the same 4 states per split
@@ -23,7 +24,8 @@
 //
 // Per page (16 tokens) and wave, both products run on bf16 MFMA:
 //   Sᵀ[16 tok × 16 col] = K[16 tok × D] · Qᵀ[D × 16 col]   (D/32 × mfma 16x16x32)
-//     col n < G is query head kvh·G + n (the GQA group), the rest is zero padding.
+//     col n < G is query head kvh·G + n (the GQA group; with G > 16, head n of the
+//     column group), the rest is zero padding.
 //     Lane (n + 16g) reads K row n, dims 8(4c+g)..+8 for c < D/32 from the tile;
 //     the result lane (n + 16g) holds S[head n][token 4g+i], i < 4.
 //   Oᵀ[D × 16 col] += Vᵀ[D × 16 tok] · Pᵀ[16 tok × 16 col]  (D/16 × mfma 16x16x16)
@@ -46,6 +48,26 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 // D/16 bf16 of one row, as a register vector (usable as an asm operand).
 template <int D>
 using RowSlice = typename std::conditional<(D / 16) == 8, u32x4_t, u32x2_t>::type;
+
+// Query-head columns: one MFMA tile holds 16 heads, so a GQA group of G > 16
+// heads is cut into ceil(G/16) column groups of at most 16 heads, each
+// computed like a KV head of its own (the column groups of one KV head read the
+// same K/V pages). For G <= 16 a KV head is one column group of G heads.
+struct ColGroup {
+  int kvh;    // KV head whose pages the column group reads
+  int head0;  // first query head of the column group
+  int cols;   // query heads in it (<= 16)
+};
+__device__ __forceinline__ int col_groups_per_kv(int G) { return (G + 15) >> 4; }
+__device__ __forceinline__ ColGroup col_group(int G, int cg) {
+  const int T = col_groups_per_kv(G);
+  ColGroup c;
+  c.kvh = cg / T;
+  const int t = cg - c.kvh * T;
+  c.head0 = c.kvh * G + 16 * t;
+  c.cols = min(16, G - 16 * t);
+  return c;
+}
 
 template <int D>
 struct PageRegs {
@@ -222,7 +244,7 @@ template <int D>
 constexpr int kTileBytes = 16 * (2 * D + 16);
 
 // Saves a wave's final state as a merge record: m[16], l[16], acc[G][D]
-// (row h of acc = head h of the group, un-normalised).
+// (row h of acc = head h of the column group, un-normalised; G = its columns).
 template <int D>
 __device__ __forceinline__ void save_state(float* rec, const WaveState<D>& st, float l_tot, int G, int n, int g) {
   constexpr int VD = D / 16;
@@ -252,11 +274,12 @@ __device__ __forceinline__ float split_inv(float L) { return L > 0.f ? 1.f / L :
 __device__ __forceinline__ float split_lse(float M, float L) { return L > 0.f ? M + __log2f(L) : kNegInf; }
 
 // Merges the NS wave states of the row (one split: the single-pass launch) in
-// wave order (record s at rec + s·rec_stride) and writes the bf16 output row.
+// wave order (record s at rec + s·rec_stride) and writes the bf16 output rows
+// of the G heads head0 .. head0 + G - 1 (one column group).
 // Thread `tid` of `nthreads` handles 4 consecutive dims of one head at a time.
 template <int D, int NS>
 __device__ __forceinline__ void merge_states(const DecodeArgs& a, const float* rec, int rec_stride, int G,
-                                             int row, int kvh, int tid, int nthreads) {
+                                             int row, int head0, int tid, int nthreads) {
   const int total4 = G * D / 4;
   for (int e = tid; e < total4; e += nthreads) {
     const int h = (e * 4) / D;
@@ -282,7 +305,7 @@ __device__ __forceinline__ void merge_states(const DecodeArgs& a, const float* r
     const float inv = split_inv(L);
     float4 o = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
     if (L == 0.f) o = make_float4(0.f, 0.f, 0.f, 0.f);
-    const int head = kvh * G + h;
+    const int head = head0 + h;
     uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)row * a.o_sb + (int64_t)head * a.o_sh + d;
     uint2 pk;
     pk.x = pack_bf16x2_hw(o.x, o.y);
@@ -292,24 +315,27 @@ __device__ __forceinline__ void merge_states(const DecodeArgs& a, const float* r
 }
 
 // LDS bytes one decode work-group uses: NW K transpose tiles, then NW merge
-// records of 32 + G·D floats.
+// records of 32 + C·D floats, C = min(G, 16) heads per column group.
 template <int D, int NW>
 constexpr size_t decode_lds_bytes(int G) {
-  return (size_t)NW * kTileBytes<D> + (size_t)NW * (32 + G * D) * sizeof(float);
+  return (size_t)NW * kTileBytes<D> + (size_t)NW * (32 + (G < 16 ? G : 16) * D) * sizeof(float);
 }
 
-// One single-pass decode work-group: (sequence, KV head) = wg, with NW waves
-// and `smem` pointing at decode_lds_bytes<D, NW>(G) bytes of LDS. Wave w walks
-// the row's pages w, w + NW, ... with PF pages in flight; the NW states are
-// merged in wave order and the bf16 output row is written.
+// One single-pass decode work-group: (sequence, column group) = wg (a column
+// group is a KV head when G <= 16), with NW waves and `smem` pointing at
+// decode_lds_bytes<D, NW>(G) bytes of LDS. Wave w walks the row's pages w,
+// w + NW, ... with PF pages in flight; the NW states are merged in wave order
+// and the bf16 output rows are written.
 template <int D, int NW, int PF>
 __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int wg, float* smem) {
   constexpr int KC = D / 32;
   constexpr int VD = D / 16;
 
-  const int G = a.num_heads / a.num_kv_heads;
-  const int kvh = wg % a.num_kv_heads;
-  const int b = wg / a.num_kv_heads;
+  const int ncg = a.num_kv_heads * col_groups_per_kv(a.num_heads / a.num_kv_heads);
+  const ColGroup cgp = col_group(a.num_heads / a.num_kv_heads, wg % ncg);
+  const int G = cgp.cols;  // heads of this column group
+  const int kvh = cgp.kvh;
+  const int b = wg / ncg;
 
   const int lane = lane_id();
   const int n = lane & 15;
@@ -328,11 +354,11 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
   int n_blocks = seq_len > 0 ? (seq_len + 15) / 16 : 0;
   n_blocks = min(n_blocks, a.max_blocks);
 
-  // Qᵀ operand: lane (n + 16g), chunk c -> q[b][kvh·G + n][8(4c+g) .. +8).
+  // Qᵀ operand: lane (n + 16g), chunk c -> q[b][head0 + n][8(4c+g) .. +8).
   uint4 qb[KC];
   {
     const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) + (int64_t)row * a.q_sb +
-                           (int64_t)(kvh * G + n) * a.q_sh;
+                           (int64_t)(cgp.head0 + n) * a.q_sh;
 #pragma unroll
     for (int c = 0; c < KC; ++c) qb[c] = (n < G) ? ld16(qrow + 8 * (4 * c + g)) : make_uint4(0, 0, 0, 0);
   }
@@ -397,7 +423,7 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
   float* merge = smem + NW * kTileBytes<D> / 4;
   save_state<D>(merge + w * wstride, st, sum_across_groups(st.l), G, n, g);
   __syncthreads();
-  merge_states<D, NW>(a, merge, wstride, G, row, kvh, threadIdx.x, NW * 64);
+  merge_states<D, NW>(a, merge, wstride, G, row, cgp.head0, threadIdx.x, NW * 64);
 }
 
 }  // namespace bvllm

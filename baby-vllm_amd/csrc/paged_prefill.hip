@@ -126,7 +126,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   const int n_pre_wgs = (int)gridDim.x - n_dec_wgs;
   if ((int)blockIdx.x >= n_pre_wgs) {
     const int dw = (int)blockIdx.x - n_pre_wgs;
-    if (dw < dec.batch * dec.num_kv_heads)
+    if (dw < dec.batch * dec.num_kv_heads * col_groups_per_kv(dec.num_heads / dec.num_kv_heads))
       decode_work_group<D, kDecodeWaves, kDecodeDepth>(dec, dw, reinterpret_cast<float*>(lds));
     return;
   }
@@ -792,7 +792,8 @@ static PrefillGrid plan_prefill(const PrefillArgs& a, int64_t CB) {
   p.prefill_wgs = p.xcd_group > 0 ? 8 * ((p.bound + p.xcd_group - 1) / p.xcd_group)
                   : p.xcd_group < 0 ? 8 * p.per_xcd
                                     : p.bound * a.num_kv_heads;
-  p.dec_wgs = a.single_query_seqs != 0 ? ((int64_t)a.num_seqs * a.num_kv_heads + 7) / 8 * 8 : 0;
+  // Decode work-groups: one per (sequence, column group), rounded up to whole XCD rounds.
+  p.dec_wgs = a.single_query_seqs != 0 ? ((int64_t)a.num_seqs * a.num_kv_heads * ((G + 15) / 16) + 7) / 8 * 8 : 0;
   return p;
 }
 

@@ -16,7 +16,10 @@
  *     k_cache = &cache[0], v_cache = &cache[1], and the page / token / head
  *     strides are those of cache[0] (cache[1] must have the same).
  *   - block_size must be 16; head_dim must be 64 or 128 (RoPE also takes 256);
- *     num_heads must be a multiple of num_kv_heads with a ratio of at most 16.
+ *     num_heads must be a multiple of num_kv_heads (any ratio; the attention
+ *     kernels compute a group of more than 16 query heads per KV head as
+ *     ceil(ratio / 16) column groups of at most 16 heads, each reading the KV
+ *     head's pages).
  *   - `stream` is a hipStream_t (NULL = the legacy default stream). Every call is
  *     asynchronous, does no host<->device copy and no host synchronisation, and
  *     allocates nothing, so it may be captured in a hipGraph.

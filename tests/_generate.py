@@ -18,12 +18,15 @@ import torch
 def hf_from(runner_model, cfg):
     """transformers' Qwen2ForCausalLM (fp32, on the GPU) loaded with our model's weights."""
     from transformers import Qwen2Config, Qwen2ForCausalLM
-    hf = Qwen2ForCausalLM(Qwen2Config(
-        vocab_size=cfg.vocab_size, hidden_size=cfg.hidden_size, intermediate_size=cfg.intermediate_size,
-        num_hidden_layers=cfg.num_hidden_layers, num_attention_heads=cfg.num_attention_heads,
-        num_key_value_heads=cfg.num_key_value_heads, rms_norm_eps=cfg.rms_norm_eps,
-        max_position_embeddings=cfg.max_position_embeddings, rope_theta=cfg.rope_theta,
-        tie_word_embeddings=False)).float().cuda().eval()
+    # Built on the GPU (its own random init is overwritten below): building a
+    # 7B-size fp32 model on the CPU first takes minutes.
+    with torch.device("cuda"):
+        hf = Qwen2ForCausalLM(Qwen2Config(
+            vocab_size=cfg.vocab_size, hidden_size=cfg.hidden_size, intermediate_size=cfg.intermediate_size,
+            num_hidden_layers=cfg.num_hidden_layers, num_attention_heads=cfg.num_attention_heads,
+            num_key_value_heads=cfg.num_key_value_heads, rms_norm_eps=cfg.rms_norm_eps,
+            max_position_embeddings=cfg.max_position_embeddings, rope_theta=cfg.rope_theta,
+            tie_word_embeddings=False)).float().eval()
     ours = {k: v.float() for k, v in runner_model.state_dict().items()}
     q, kv = cfg.num_attention_heads * cfg.head_dim, cfg.num_key_value_heads * cfg.head_dim
     sd = {"model.embed_tokens.weight": ours["model.embed_tokens.weight"],
@@ -112,3 +115,52 @@ def compare_with_checker(tokens, our_logits, want_logits, max_tol, mean_tol):
                 gap = float(want[pos, best[pos]] - want[pos, tok])
                 assert gap <= 2 * float(row_max[pos]), (pos, tok, int(best[pos]), gap, float(row_max[pos]))
     return exact, total, worst_max, worst_mean
+
+
+@torch.no_grad()
+def bf16_cpu_checker_logits(hf_fp32, prompts, tokens):
+    """A second, bf16 checker: the same transformers model cast to bf16 and run
+    on the host CPU (oneDNN bf16 GEMMs with fp32 accumulation; bf16 activations,
+    residual and logits, as the reference's design), teacher-forced on `tokens`.
+    Its disagreement with the fp32 checker is the precision floor of bf16
+    arithmetic on the model. The rotary frequencies stay fp32, as both
+    implementations compute them. Moves the model to the CPU."""
+    inv = hf_fp32.model.rotary_emb.inv_freq.detach().clone().cpu()
+    hf = hf_fp32.to(torch.bfloat16).to("cpu")
+    hf.model.rotary_emb.inv_freq = inv
+    out = []
+    for p, t in zip(prompts, tokens):
+        ids = torch.tensor([list(p) + list(t[:-1])])
+        out.append(hf(ids).logits[0, len(p) - 1:].float())
+    return out
+
+
+def argmax_agreement(a_logits, b_logits):
+    """Positions where the two logits rows have the same argmax, and the total."""
+    same = sum(int((a.argmax(-1) == b.argmax(-1)).sum()) for a, b in zip(a_logits, b_logits))
+    return same, sum(a.shape[0] for a in a_logits)
+
+
+def compare_runs(tokens_a, logits_a, tokens_b, logits_b, max_tol):
+    """Two greedy runs of our engine on the same prompts (different launch
+    choices). Up to and including the first position where their tokens
+    differ, both runs saw the same inputs: there each pair of logits rows must
+    agree within max_tol (max-abs), and at that first differing position each
+    run's token must lead the other's by at most twice the rows' measured
+    difference (a near-tie). Returns (positions compared, worst max-abs,
+    prompts that diverged)."""
+    compared, worst, diverged = 0, 0.0, 0
+    for ta, la, tb, lb in zip(tokens_a, logits_a, tokens_b, logits_b):
+        n = next((i for i, (x, y) in enumerate(zip(ta, tb)) if x != y), len(ta))
+        for pos in range(min(n + 1, len(ta))):
+            d = float((la[pos] - lb[pos]).abs().max())
+            worst = max(worst, d)
+            compared += 1
+            assert d <= max_tol, (pos, d)
+        if n < len(ta):
+            diverged += 1
+            d = float((la[n] - lb[n]).abs().max())
+            lead_a = float(la[n][ta[n]] - la[n][tb[n]])
+            lead_b = float(lb[n][tb[n]] - lb[n][ta[n]])
+            assert 0 <= lead_a <= 2 * d and 0 <= lead_b <= 2 * d, (n, lead_a, lead_b, d)
+    return compared, worst, diverged

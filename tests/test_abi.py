@@ -105,9 +105,9 @@ def test_host_side_argument_rejection():
     # 28 heads over 5 KV heads
     assert h.bvllm_rope_kv_append(None, 0, 0, None, 0, 0, None, 0, 0, None, 0, None, 0,
                                   None, None, 0, 0, 0, None, 1, 28, 5, 128, None) == bad
-    # GQA group above 16
+    # 34 query heads over 4 KV heads (GQA groups above 16 are accepted: 34 over 2 is)
     assert h.bvllm_paged_decode(None, 0, 0, None, None, 0, 0, 0, 0, None, 0, 0, None, 1.0,
-                                None, 0, 0, None, 1, 1, 1, 34, 2, 128, 16, 0, None) == bad
+                                None, 0, 0, None, 1, 1, 1, 34, 4, 128, 16, 0, None) == bad
     assert b"invalid argument" in h.bvllm_error_string(bad)
     # waves must be 0 or 4 (8 was accepted by an earlier ABI and is refused now)
     for waves in (5, 8):

@@ -163,6 +163,35 @@ def test_other_head_configs(hkv, group, d):
         assert_attn_close(actual, _oracle(q, kv_cache, bt, lens, d ** -0.5))
 
 
+# GQA groups above one 16-column MFMA tile (MQA-style layouts): the group is cut
+# into 16-head column groups; the reference pads any group
+# (babyvllm/kernels/paged_attn.py:275).
+_WIDE_GROUPS = [(1, 32, 128), (1, 64, 128), (2, 24, 64), (1, 17, 64), (3, 20, 128)]
+
+
+@pytest.mark.parametrize("hkv,group,d", _WIDE_GROUPS)
+def test_gqa_groups_above_16(hkv, group, d):
+    lens = [1, 40, 200, 513, 0, 1100]
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, hkv=hkv, group=group, d=d, seed=group)
+    want = _oracle(q, kv_cache, bt, lens, d ** -0.5)
+    for part in (0, None, 3, 8):
+        actual = _kernel()(q, kv_cache, bt, seq_lens, d ** -0.5, max_seq_len=1200, partition_blocks=part)
+        assert_attn_close(actual, want, rows=_live(lens))
+        assert actual[4].abs().max() == 0
+
+
+@pytest.mark.parametrize("hkv,group,d", _WIDE_GROUPS[:3])
+def test_gqa_groups_above_16_launch_choices_agree(hkv, group, d):
+    lens = [700, 33, 0, 1500]
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, width=128, seed=7 * group, hkv=hkv, group=group, d=d)
+    scale = d ** -0.5
+    for partition in (4, 0, 2):
+        outs = _modes(q, kv_cache, bt, seq_lens, scale, 2048, partition)
+        for name, out in outs.items():
+            assert torch.equal(out, outs["auto"]), name
+        assert_attn_close(outs["auto"], _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
+
+
 def test_strided_q_view_into_fused_qkv():
     lens = [100, 7]
     q, kv_cache, bt, seq_lens = make_decode_inputs(lens, seed=5)

@@ -380,3 +380,30 @@ def test_key_split_with_rising_scores(growth):
     assert_attn_close(_kernel()(q, kv_cache, md, 128 ** -0.5), expected)
     with tuned(_SHORT_GRID, 1):
         assert_attn_close(_kernel()(q, kv_cache, md, 128 ** -0.5), expected)
+
+
+# ------------------------------------------ GQA groups above 16 query heads per KV head
+
+# The reference's prefill takes any H % Hkv == 0 (babyvllm/kernels/paged_prefill.py:114-115):
+# fresh, prefix and mixed steps (the decode rows of a mixed step run on the decode
+# work-groups, cut into 16-head column groups).
+WIDE_GROUP_CASES = {
+    "fresh": [(0, 128), (0, 17), (0, 1)],
+    "prefix": [(37, 20), (100, 130), (16, 2)],
+    "mixed": [(0, 40), (200, 1), (63, 1), (500, 1), (16, 16)],
+    "short grid": [(1024, 128)] * 2,
+}
+
+
+@pytest.mark.parametrize("name", list(WIDE_GROUP_CASES))
+@pytest.mark.parametrize("hkv,group,d", [(1, 32, 128), (1, 64, 128), (2, 24, 64), (1, 17, 64)])
+def test_gqa_groups_above_16(name, hkv, group, d):
+    specs = WIDE_GROUP_CASES[name]
+    q, kv_cache, md = build_prefill_case(specs, hkv, group, d, seed=group + len(specs))
+    expected = _oracle(q, kv_cache, md, group)
+    actual = _kernel()(q, kv_cache, md, d ** -0.5)
+    assert not torch.isnan(actual).any()
+    assert_attn_close(actual, expected)
+    with tuned(_SHORT_GRID, 1):
+        walk = _kernel()(q, kv_cache, md, d ** -0.5)
+    assert_attn_close(walk, expected)

@@ -134,3 +134,54 @@ def test_noalloc_refuses_a_plan_beyond_its_scratch():
     assert b"BVLLM_NOALLOC_SCRATCH_BYTES" in L.lib().bvllm_error_string(rc)
     torch.cuda.synchronize()
     assert torch.isnan(out).all()  # nothing was launched
+
+
+_CAPTURE_FIRST_CALL = r"""
+import sys
+sys.path[:0] = [{repo!r}, {repo!r} + "/baby-vllm_amd", {repo!r} + "/tests"]
+import torch
+from tests import test_zz_no_alloc as t
+from tests._cases import make_decode_inputs
+
+scale = 128 ** -0.5
+lens = [1900, 1500, 1920, 700, 1920, 33, 1800, 1024]
+q, kv, bt, sl = make_decode_inputs(lens, width=120, seed=21)
+plan = t._plan(8, 120, 1920)
+assert plan[0] > 1
+side = torch.cuda.Stream()
+side.wait_stream(torch.cuda.current_stream())
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.stream(side):
+    with torch.cuda.graph(graph, stream=side):
+        # The process's first call of the entry point: its scratch lookup
+        # happens inside the capture.
+        rc, out = t._call("bvllm_paged_decode_noalloc", q, kv, bt, sl, scale, plan)
+torch.cuda.current_stream().wait_stream(side)
+torch.cuda.synchronize()
+t._lib().check(rc, "bvllm_paged_decode_noalloc under capture")
+g = torch.Generator(device="cuda").manual_seed(5)
+for replay in range(4):
+    q.copy_(torch.randn(q.shape, device="cuda", dtype=q.dtype, generator=g))
+    if replay == 2:
+        sl.copy_(torch.tensor([16, 1920, 1, 0, 500, 1919, 64, 1234], dtype=torch.int32))
+    graph.replay()
+    torch.cuda.synchronize()
+    want, _ = t._with_workspace(q, kv, bt, sl, scale, plan)  # eager, between replays
+    torch.cuda.synchronize()
+    assert torch.equal(out, want), f"replay {{replay}} differs from the workspace entry point"
+print("CAPTURE_OK", flush=True)
+"""
+
+
+def test_noalloc_first_call_inside_graph_capture_then_replays():
+    # A fresh process, so that the capture holds the first call (and the
+    # scratch address lookup); every replay is compared bit for bit with the
+    # workspace entry point run eagerly between replays.
+    import os
+    import subprocess
+    import sys
+
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = _CAPTURE_FIRST_CALL.format(repo=repo)
+    p = subprocess.run([sys.executable, "-c", code], cwd=repo, capture_output=True, text=True, timeout=300)
+    assert p.returncode == 0 and "CAPTURE_OK" in p.stdout, p.stdout[-2000:] + p.stderr[-4000:]
