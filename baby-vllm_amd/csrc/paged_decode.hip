@@ -67,25 +67,32 @@ __device__ __forceinline__ void load_chain(ChainRegs& r, const float* lse, const
   }
 }
 
-__device__ __forceinline__ float chain_max(const ChainRegs& r) {
+// Entries at or past `live` (a uniform count) are empty (lse -inf, output 0)
+// and are not visited: an empty entry leaves the maximum and the sums
+// bit-identical (weight 2^-inf = 0, fma(0, 0, x) = x), so skipping changes no
+// bit, only the length of the dependent chains.
+__device__ __forceinline__ float chain_max(const ChainRegs& r, int live = kChain) {
   float M = kNegInf;
 #pragma unroll
-  for (int k = 0; k < kChain; ++k) M = fmaxf(M, r.l[k]);
+  for (int k = 0; k < kChain; ++k)
+    if (k < live) M = fmaxf(M, r.l[k]);
   return M;
 }
 
 // The chain's fma sums in group order.
-__device__ __forceinline__ void chain_sums(const ChainRegs& r, float M, float4& num, float& den) {
+__device__ __forceinline__ void chain_sums(const ChainRegs& r, float M, float4& num, float& den, int live = kChain) {
   num = make_float4(0.f, 0.f, 0.f, 0.f);
   den = 0.f;
 #pragma unroll
   for (int k = 0; k < kChain; ++k) {
-    const float wgt = fast_exp2(r.l[k] - M);
-    num.x = __builtin_fmaf(wgt, r.x[k].x, num.x);
-    num.y = __builtin_fmaf(wgt, r.x[k].y, num.y);
-    num.z = __builtin_fmaf(wgt, r.x[k].z, num.z);
-    num.w = __builtin_fmaf(wgt, r.x[k].w, num.w);
-    den += wgt;
+    if (k < live) {  // a guarded body, not a break: every index stays a constant (registers, not scratch)
+      const float wgt = fast_exp2(r.l[k] - M);
+      num.x = __builtin_fmaf(wgt, r.x[k].x, num.x);
+      num.y = __builtin_fmaf(wgt, r.x[k].y, num.y);
+      num.z = __builtin_fmaf(wgt, r.x[k].z, num.z);
+      num.w = __builtin_fmaf(wgt, r.x[k].w, num.w);
+      den += wgt;
+    }
   }
 }
 
@@ -102,7 +109,9 @@ __device__ __forceinline__ void store_reduced(const DecodeArgs& a, int64_t bh, i
 
 // At most kChain group results per (row, head): one thread per (row, head,
 // 4 dims). FOLD: the workspace holds one partial per split (at most kChain of
-// them), folded here into groups of kSplitGroup first.
+// them), folded here into groups of kSplitGroup first. Entries past the np
+// partials are empty and are not visited (folding an empty split changes
+// nothing), so the dependent chains are as long as the live entries.
 template <int D, bool FOLD>
 __global__ __launch_bounds__(256) void decode_reduce_small_kernel(DecodeArgs a, int64_t items) {
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -112,37 +121,39 @@ __global__ __launch_bounds__(256) void decode_reduce_small_kernel(DecodeArgs a, 
   const int np = a.num_partials;
   ChainRegs r;
   load_chain(r, a.part_lse + bh * np, a.part_out + bh * np * D + d, D, 0, np);
+  int live = np;
   if constexpr (FOLD) {
     // Level 2 in place: group q's result replaces entry q (q < kChain / 4).
+    // Guarded bodies, not breaks: every index stays a constant (registers, not scratch).
 #pragma unroll
     for (int q = 0; q < kChain / kSplitGroup; ++q) {
-      GroupFold f;
-      float4 gx = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (q * kSplitGroup < np) {
+        GroupFold f;
+        float4 gx = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-      for (int k = 0; k < kSplitGroup; ++k) {
-        const int s = q * kSplitGroup + k;
-        float wa, wb;
-        group_fold_weights(f, r.l[s], wa, wb);
-        gx.x = group_fold_value(gx.x, r.x[s].x, wa, wb);
-        gx.y = group_fold_value(gx.y, r.x[s].y, wa, wb);
-        gx.z = group_fold_value(gx.z, r.x[s].z, wa, wb);
-        gx.w = group_fold_value(gx.w, r.x[s].w, wa, wb);
+        for (int k = 0; k < kSplitGroup; ++k) {
+          const int s = q * kSplitGroup + k;
+          if (s < np) {
+            float wa, wb;
+            group_fold_weights(f, r.l[s], wa, wb);
+            gx.x = group_fold_value(gx.x, r.x[s].x, wa, wb);
+            gx.y = group_fold_value(gx.y, r.x[s].y, wa, wb);
+            gx.z = group_fold_value(gx.z, r.x[s].z, wa, wb);
+            gx.w = group_fold_value(gx.w, r.x[s].w, wa, wb);
+          }
+        }
+        const float inv = group_inv(f);
+        r.l[q] = group_lse(f);
+        r.x[q] = make_float4(gx.x * inv, gx.y * inv, gx.z * inv, gx.w * inv);
       }
-      const float inv = group_inv(f);
-      r.l[q] = group_lse(f);
-      r.x[q] = make_float4(gx.x * inv, gx.y * inv, gx.z * inv, gx.w * inv);
     }
-#pragma unroll
-    for (int q = kChain / kSplitGroup; q < kChain; ++q) {
-      r.l[q] = kNegInf;
-      r.x[q] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    live = (np + kSplitGroup - 1) / kSplitGroup;
   }
-  float M = chain_max(r);
+  float M = chain_max(r, live);
   if (M == kNegInf) M = 0.f;
   float4 num;
   float den;
-  chain_sums(r, M, num, den);
+  chain_sums(r, M, num, den, live);
   store_reduced(a, bh, d, num, den);
 }
 
@@ -364,7 +375,8 @@ static hipError_t launch_stream(const DecodeArgs& a, int64_t items, hipStream_t 
 template <int D>
 static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
   DecodeArgs a = args;
-  const DecodePlan p = decode_plan(a.batch, a.num_kv_heads, a.num_splits, a.blocks_per_split);
+  const int64_t ncg = decode_col_groups(a);
+  const DecodePlan p = decode_plan(a.batch, (int32_t)ncg, a.num_splits, a.blocks_per_split);
   a.item_order = tuning(kTuneDecodeOrder) == 1 ? 1 : 0;
   if (p.single_pass && tuning(kTuneDecodeSinglePassStream) == 0) {
     constexpr int NW = 4;
