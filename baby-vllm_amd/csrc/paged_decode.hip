@@ -14,10 +14,10 @@
 
 namespace bvllm {
 
-template <int D, int NW, int PF>
+template <int D, int NW, int PF, bool EAGER>
 __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
   extern __shared__ float smem[];
-  decode_work_group<D, NW, PF>(a, blockIdx.x, smem);
+  decode_work_group<D, NW, PF, EAGER>(a, blockIdx.x, smem);
 }
 
 // Two waves per split, or per group of splits (PAIR), four pages in flight each.
@@ -379,16 +379,20 @@ static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
   const DecodePlan p = decode_plan(a.batch, (int32_t)ncg, a.num_splits, a.blocks_per_split);
   a.item_order = tuning(kTuneDecodeOrder) == 1 ? 1 : 0;
   if (p.single_pass && tuning(kTuneDecodeSinglePassStream) == 0) {
+    // One page in flight per wave, the next requested as soon as it has
+    // landed: more requests in flight lower the rate this access pattern gets
+    // from HBM (B64 x 1920: 43.0 us, against 44.5 with two pages in flight
+    // requested after each page is computed, 45.1 with three, 46.9 with four).
     constexpr int NW = 4;
     const int G = a.num_heads / a.num_kv_heads;
     const size_t smem = decode_lds_bytes<D, NW>(G);
     if (smem > 160 * 1024) return hipErrorInvalidValue;
     static std::atomic<bool> done[64] = {};
-    hipError_t err = allow_lds(&paged_decode_kernel<D, NW, 2>, done, 160 * 1024);
+    hipError_t err = allow_lds(&paged_decode_kernel<D, NW, 1, true>, done, 160 * 1024);
     if (err != hipSuccess) return err;
     const int64_t wgs = (int64_t)a.batch * decode_col_groups(a);
     if (wgs > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((paged_decode_kernel<D, NW, 2>), dim3((unsigned)wgs), dim3(NW * 64), smem, stream, a);
+    hipLaunchKernelGGL((paged_decode_kernel<D, NW, 1, true>), dim3((unsigned)wgs), dim3(NW * 64), smem, stream, a);
     return hipGetLastError();
   }
   a.splits_per_item = p.single_pass ? 1 : p.splits_per_item;

@@ -86,9 +86,11 @@ __device__ __forceinline__ bool find_query_block(const PrefillArgs& a, int CB, i
   return false;
 }
 
-// Waves and pages in flight of the decode work-groups of a mixed step.
+// Waves and pages in flight of the decode work-groups of a mixed step: one page
+// per wave, the next requested as soon as it has landed (1 x 512 + 63 decodes:
+// 29.3 us, against 29.9 with two pages requested after each page is computed).
 constexpr int kDecodeWaves = 4;
-constexpr int kDecodeDepth = 2;
+constexpr int kDecodeDepth = 1;
 
 // MB: groups of several blocks per work-group, launched only when every
 // sequence's keys fit two 64-key tiles (the kernel has no streaming path then).
@@ -127,7 +129,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   if ((int)blockIdx.x >= n_pre_wgs) {
     const int dw = (int)blockIdx.x - n_pre_wgs;
     if (dw < dec.batch * dec.num_kv_heads * col_groups_per_kv(dec.num_heads / dec.num_kv_heads))
-      decode_work_group<D, kDecodeWaves, kDecodeDepth>(dec, dw, reinterpret_cast<float*>(lds));
+      decode_work_group<D, kDecodeWaves, kDecodeDepth, true>(dec, dw, reinterpret_cast<float*>(lds));
     return;
   }
 
