@@ -366,7 +366,10 @@ static hipError_t launch_stream_pf(const DecodeArgs& a, int64_t items, hipStream
 
 // Two pages in flight per streaming wave. (Four do not fit the register file
 // next to the four states: the compiler then parks registers that in-flight
-// loads still write.)
+// loads still write. One, requested as soon as the previous page has landed,
+// as in the single pass: B1 x 32768 24.97 against 24.92 us, and slower for
+// B8's group waves, 31.2 against 30.8 us: these launches wait on latency,
+// not on the DRAM.)
 template <int D, bool GROUP>
 static hipError_t launch_stream(const DecodeArgs& a, int64_t items, hipStream_t stream) {
   return launch_stream_pf<D, 2, GROUP>(a, items, stream);
