@@ -326,9 +326,9 @@ constexpr size_t decode_lds_bytes(int G) {
 // decode_lds_bytes<D, NW>(G) bytes of LDS. Wave w walks the row's pages w,
 // w + NW, ... with PF pages in flight; the NW states are merged in wave order
 // and the bf16 output rows are written.
-// EAGER: page k+PF is requested as soon as page k has landed, before page k is
-// computed (PF+1 register sets), instead of after; the page order, so the
-// arithmetic, is the same either way.
+// EAGER (PF = 1): page k+1 is requested as soon as page k has landed, before
+// page k is computed (two register sets), instead of after; the page order, so
+// the arithmetic, is the same either way.
 template <int D, int NW, int PF, bool EAGER = false>
 __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int wg, float* smem) {
   constexpr int KC = D / 32;
@@ -393,40 +393,64 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
     const int slot_ent = min(max(ent, 0), a.num_pages - 1);
     auto phys = [&](int k) -> int64_t { return (int64_t)__builtin_amdgcn_readlane(slot_ent, k); };
 
+    if constexpr (EAGER) {
+      // One page in flight: page j+1 is requested as soon as page j has
+      // landed (before page j is computed), and only while there is one: no
+      // load is issued past the wave's last page, so the wave never waits at
+      // its end for a page nobody computes. With at most one page outstanding
+      // every wait is vmcnt(0).
+      static_assert(PF == 1, "the eager walk keeps one page in flight");
+      PageRegs<D> r[2];
+      {
+        const int64_t p = phys(0) * a.c_sb;
+        load_page<D>(r[0], kc + p, vc + p, off);
+      }
+      for (int k = 0; k < here; k += 2) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          if (k + i < here) {
+            wait_page<0, D>(r[i]);
+            if (k + i + 1 < here) {
+              const int64_t pn = phys(k + i + 1) * a.c_sb;
+              load_page<D>(r[i ^ 1], kc + pn, vc + pn, off);
+            }
+            const int page = first + NW * (base + k + i);
+            process_page<D>(st, r[i], qb, tile, n, g, page * 16 + 4 * g, seq_len, a.scale_log2);
+          }
+        }
+      }
+      // Every load issued above was waited for; this wait (immediate) keeps
+      // that visible in the code's structure as well.
+#pragma unroll
+      for (int i = 0; i < 2; ++i) wait_page<0, D>(r[i]);
+      continue;
+    }
     // PF pages in flight per wave: page k+PF is requested as soon as page k has
-    // landed (EAGER) or has been computed. Loads are issued unconditionally
-    // (page index clamped into the wave's range) and the page count is padded
-    // to a multiple of the register sets with fully masked pages, so every
-    // wait counts exactly PF-1 younger pages.
-    constexpr int RS = EAGER ? PF + 1 : PF;  // register sets
-    PageRegs<D> r[RS];
+    // been computed. Loads are issued unconditionally (page index clamped into
+    // the wave's range) and the page count is padded to a multiple of PF with
+    // fully masked pages, so every wait counts exactly PF-1 younger pages.
+    PageRegs<D> r[PF];
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int64_t p = phys(min(i, here - 1)) * a.c_sb;
       load_page<D>(r[i], kc + p, vc + p, off);
     }
-    const int padded = (here + RS - 1) / RS * RS;
-    for (int k = 0; k < padded; k += RS) {
+    const int padded = (here + PF - 1) / PF * PF;
+    for (int k = 0; k < padded; k += PF) {
 #pragma unroll
-      for (int i = 0; i < RS; ++i) {
+      for (int i = 0; i < PF; ++i) {
         wait_page<(PF - 1) * kLoadsPerPage, D>(r[i]);
         const int page = first + NW * (base + k + i);
         const int limit = (k + i < here) ? seq_len : 0;
+        process_page<D>(st, r[i], qb, tile, n, g, page * 16 + 4 * g, limit, a.scale_log2);
         const int64_t pn = phys(min(k + i + PF, here - 1)) * a.c_sb;
-        if constexpr (EAGER) {
-          // r[(i + PF) % RS] held page k+i-1, computed in the previous step.
-          load_page<D>(r[(i + PF) % RS], kc + pn, vc + pn, off);
-          process_page<D>(st, r[i], qb, tile, n, g, page * 16 + 4 * g, limit, a.scale_log2);
-        } else {
-          process_page<D>(st, r[i], qb, tile, n, g, page * 16 + 4 * g, limit, a.scale_log2);
-          load_page<D>(r[i], kc + pn, vc + pn, off);
-        }
+        load_page<D>(r[i], kc + pn, vc + pn, off);
       }
     }
     // Drain: the loads issued for pages past the end must land before their
     // registers are reused.
 #pragma unroll
-    for (int i = 0; i < RS; ++i) wait_page<0, D>(r[i]);
+    for (int i = 0; i < PF; ++i) wait_page<0, D>(r[i]);
   }
 
   // Merge records (m[16], l[16], acc[G][D] per wave) follow the NW K tiles.
