@@ -586,14 +586,17 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
 
   // Half step x (= 2j + h) on S(x) in Sc, producing S(x+1) in Sn.
   auto half_step = [&](const int x, f32x4_t (&Sc)[QT][2], f32x4_t (&Sn)[QT][2], const int kbuf_next,
-                       const int h_next, const int vbuf, const int h) __attribute__((always_inline)) {
-    // One code path for every computed half: the last half also forms
-    // Sᵀ(x+1) (in-bounds LDS reads of a buffer it never uses), so that the
-    // accumulators have a single definition per step.
+                       const int h_next, const int vbuf, const int h, const bool next = true)
+                       __attribute__((always_inline)) {
+    // One code path for every computed half of the streaming walk: its last
+    // half also forms Sᵀ(x+1) (in-bounds LDS reads of a buffer it never
+    // uses), so that the accumulators have a single definition per step. The
+    // short path passes next = false for a wave's last half, which skips that
+    // product (64 x 128: 36.0 -> 35.6 us).
     uint4 pb[QT];
     if (x < wave_halves) {
       __builtin_amdgcn_s_setprio(1);
-      qk(Sn, kbuf_next, h_next);
+      if (next) qk(Sn, kbuf_next, h_next);
       softmax_p(Sc, pb);
       // P is formed here, under the QKᵀ MFMAs and beside the max, not sunk
       // past the branches below.
@@ -601,7 +604,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
       for (int ct = 0; ct < QT; ++ct) asm volatile("" ::"v"(pb[ct].x), "v"(pb[ct].y), "v"(pb[ct].z), "v"(pb[ct].w));
       __builtin_amdgcn_s_setprio(0);
       raise_max(Sc, pb);
-      if (needs_mask(32 * (x + 1))) mask(Sn, 32 * (x + 1));
+      if (next && needs_mask(32 * (x + 1))) mask(Sn, 32 * (x + 1));
       __builtin_amdgcn_s_setprio(1);
       pv(pb, vbuf, h);
       __builtin_amdgcn_s_setprio(0);
@@ -699,10 +702,11 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   } else if (short_wg) {
     // Every tile is in LDS; the last half's Sᵀ(x+1) reads K buffer 0 (in
     // bounds, never used).
-    half_step(0, S0, S1, 0, 1, 0, 0);
-    half_step(1, S1, S0, 1, 0, 0, 1);
-    half_step(2, S0, S1, 1, 1, 1, 0);
-    half_step(3, S1, S0, 0, 0, 1, 1);
+    // The wave's last computed half forms no Sᵀ of the half after it.
+    half_step(0, S0, S1, 0, 1, 0, 0, 1 < wave_halves);
+    half_step(1, S1, S0, 1, 0, 0, 1, 2 < wave_halves);
+    half_step(2, S0, S1, 1, 1, 1, 0, 3 < wave_halves);
+    half_step(3, S1, S0, 0, 0, 1, 1, false);
   } else {
     // Two tiles per iteration, so that buffer numbers are constants.
     for (int j = 0; j < n_tiles; j += 2) {
