@@ -281,8 +281,8 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
       // The wave's pages in order: q = 8j + 4(i/2) + 2w + (i mod 2) for ring
       // slot i, state i mod 2 (global state 2w + i mod 2).
       if (!GROUP && here <= 8) {
-        // Every page of the chunk fits the four slots: no further load (none
-        // past the chunk's end to wait for), slot i waits for itself only.
+        // One split whose pages all fit the four slots: no further load (none
+        // past the split's end to wait for), slot i waits for itself only.
         // (The loads are issued on each side of this branch, so no register
         // of a load in flight crosses it.)
 #pragma unroll
@@ -293,16 +293,6 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
 #pragma unroll
         for (int i = 0; i < PF; ++i) {
           const int quad = 4 * (i >> 1);
-          if constexpr (GROUP) {
-            if ((i & 1) == 0 && quad < here && base + quad == next_start) {
-              pair_exchange(xb);
-              xb ^= 1;
-              if (w == 0) finish_split(cur);
-              ++cur;
-              next_start = (cur + 1 < j1) ? next_start + bps : INT_MAX;
-              any = false;
-            }
-          }
           if (i == 0) wait_page<3 * kLoadsPerPage, D>(r[0]);
           else if (i == 1) wait_page<2 * kLoadsPerPage, D>(r[1]);
           else if (i == 2) wait_page<kLoadsPerPage, D>(r[2]);

@@ -700,9 +700,8 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
       }
     }
   } else if (short_wg) {
-    // Every tile is in LDS; the last half's Sᵀ(x+1) reads K buffer 0 (in
-    // bounds, never used).
-    // The wave's last computed half forms no Sᵀ of the half after it.
+    // Every tile is in LDS. The wave's last computed half forms no Sᵀ of the
+    // half after it.
     half_step(0, S0, S1, 0, 1, 0, 0, 1 < wave_halves);
     half_step(1, S1, S0, 1, 0, 0, 1, 2 < wave_halves);
     half_step(2, S0, S1, 1, 1, 1, 0, 3 < wave_halves);
