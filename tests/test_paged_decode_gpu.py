@@ -291,6 +291,26 @@ def test_launch_choices_other_head_configs(hkv, group, d):
         assert_attn_close(outs["auto"], _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
 
 
+def test_single_pass_walk_lengths_around_the_table_slices():
+    """The single pass's page walk (wave w of 4 takes pages w, w+4, ...; one page
+    in flight, none requested past the wave's last page; the row's table entries
+    come in slices of 64 per wave) on rows whose per-wave page counts sit at and
+    just past a slice (4096 tokens: 64 pages per wave; 4097: 65 for wave 0) and on
+    rows of one to five pages (waves with no page or one): the same bits as the
+    single pass on streaming waves, and the oracle's values."""
+    lens = [4096, 4097, 4112, 4113, 1, 17, 33, 49, 65, 0]
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, seed=41)
+    scale = HEAD_DIM ** -0.5
+    from babyvllm.kernels import _lib
+
+    wg = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=max(lens), partition_blocks=0)
+    with tuned(_lib.TUNE_DECODE_SINGLE_PASS_STREAM, 1):
+        st = _kernel()(q, kv_cache, bt, seq_lens, scale, max_seq_len=max(lens), partition_blocks=0)
+    assert torch.equal(wg, st)
+    assert wg[len(lens) - 1].abs().max() == 0
+    assert_attn_close(wg, _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
+
+
 @pytest.mark.parametrize("partition", [0, 1, 4])
 def test_scores_rising_along_the_row(partition):
     """Key norms growing with position: the running max of every split is
