@@ -112,6 +112,43 @@ def test_ties_nan_and_infinities_across_batches(dtype):
     assert torch.equal(out.cpu(), ds.greedy_argmax(x.cpu()))
 
 
+def test_fp32_ties_and_nan_around_the_chunk_boundaries():
+    """fp32 rows are cut into 2,048-column chunks (bf16 rows into 4,096): ties
+    straddling those boundaries go to the lower column, -0.0 ties +0.0 across
+    chunks, and a NaN in the partial last chunk beats every number."""
+    vocab = 3 * 2048 + 40                              # a partial last chunk
+    x = torch.randn(6, vocab, device="cuda", dtype=torch.float32)
+    x[0, [2047, 2048]] = 9.0                           # straddles the first boundary
+    x[1, [4100, 4095]] = 9.0                           # later chunk first in the list
+    x[2] = -1.0
+    x[2, 5000] = 0.0
+    x[2, 300] = -0.0                                   # -0.0 ties +0.0, lower column
+    x[3, vocab - 1] = float("nan")                     # NaN in the partial chunk
+    x[3, 10] = 100.0
+    x[4] = -float("inf")
+    x[4, vocab - 3] = -1e30                            # the only finite value, last chunk
+    x[5, [6143, 6144, 6150]] = 7.0                     # the last full chunk and the partial one
+    out = torch.empty(6, dtype=torch.int64, device="cuda")
+    _argmax()(x, out)
+    assert out.tolist() == [2047, 4095, 300, vocab - 1, vocab - 3, 6143]
+    assert torch.equal(out.cpu(), ds.greedy_argmax(x.cpu()))
+
+
+def test_more_rows_than_one_launch_takes():
+    """Rows beyond the 65,535 of one launch's grid continue in a second launch."""
+    rows, vocab = 70_000, 24
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(rows, vocab, generator=g).to(torch.bfloat16)
+    x[65_535, [3, 17]] = 50.0                           # first row of the second launch
+    x[65_534, 23] = float("nan")                        # last row of the first launch
+    xd = x.to("cuda")
+    out = torch.full((rows,), -1, dtype=torch.int64, device="cuda")
+    _argmax()(xd, out)
+    exp = ds.greedy_argmax(x)
+    assert int(exp[65_535]) == 3 and int(exp[65_534]) == 23
+    assert torch.equal(out.cpu(), exp)
+
+
 def test_unaligned_rows_take_the_two_stage_path_with_the_same_answers():
     vocab = 20001                                       # 40,002 bytes per row: not 16-byte aligned
     x = torch.zeros(4, vocab, device="cuda", dtype=torch.bfloat16)
