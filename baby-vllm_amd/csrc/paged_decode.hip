@@ -388,9 +388,8 @@ static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
     // requested after each page is computed, 45.1 with three, 46.9 with four;
     // 42.4 us once no load is issued past a wave's last page).
     constexpr int NW = 4;
-    const int G = a.num_heads / a.num_kv_heads;
-    const size_t smem = decode_lds_bytes<D, NW>(G);
-    if (smem > 160 * 1024) return hipErrorInvalidValue;
+    constexpr size_t smem = decode_lds_bytes<D, NW>();
+    static_assert(smem <= 160 * 1024, "single-pass work-group LDS");
     static std::atomic<bool> done[64] = {};
     hipError_t err = allow_lds(&paged_decode_kernel<D, NW, 1, true>, done, 160 * 1024);
     if (err != hipSuccess) return err;

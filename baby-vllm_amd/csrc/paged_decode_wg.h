@@ -243,24 +243,19 @@ __device__ __forceinline__ void process_page(WaveState<D>& st, const PageRegs<D>
 template <int D>
 constexpr int kTileBytes = 16 * (2 * D + 16);
 
-// Saves a wave's final state as a merge record: m[16], l[16], acc[G][D]
-// (row h of acc = head h of the column group, un-normalised; G = its columns).
+// A wave's final state as a merge record, per lane L = n + 16g: m at [L], the
+// row sum over the four lane groups (the same in all four) at [64 + L], then
+// accumulator vector c (head n, dims VD·(4g + i) + c for its elements i) at
+// [128 + 4·(64c + L)]: 16-byte stores in lane order, no LDS bank conflicts.
 template <int D>
-__device__ __forceinline__ void save_state(float* rec, const WaveState<D>& st, float l_tot, int G, int n, int g) {
-  constexpr int VD = D / 16;
-  constexpr int OD = D / 4;
-  if (g == 0) {
-    rec[n] = st.m;
-    rec[16 + n] = l_tot;
-  }
-  if (n < G) {
-    float* dst = rec + 32 + n * D + OD * g;
+constexpr int kMergeRecFloats = (2 + 4 * (D / 16)) * 64;
+
+template <int D>
+__device__ __forceinline__ void save_state(float* rec, const WaveState<D>& st, int lane) {
+  rec[lane] = st.m;
+  rec[64 + lane] = sum_across_groups(st.l);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int c = 0; c < VD; ++c) dst[VD * i + c] = st.acc[c][i];
-    }
-  }
+  for (int c = 0; c < D / 16; ++c) *reinterpret_cast<f32x4_t*>(rec + 128 + (64 * c + lane) * 4) = st.acc[c];
 }
 
 // Merge arithmetic of NS per-state results of one split, in state order:
@@ -274,56 +269,65 @@ __device__ __forceinline__ float split_inv(float L) { return L > 0.f ? 1.f / L :
 __device__ __forceinline__ float split_lse(float M, float L) { return L > 0.f ? M + __log2f(L) : kNegInf; }
 
 // Merges the NS wave states of the row (one split: the single-pass launch) in
-// wave order (record s at rec + s·rec_stride) and writes the bf16 output rows
-// of the G heads head0 .. head0 + G - 1 (one column group).
-// Thread `tid` of `nthreads` handles 4 consecutive dims of one head at a time.
+// wave order (record s at rec + s·kMergeRecFloats) for element e of every
+// lane's accumulator vectors, and writes those dims of the bf16 output rows of
+// the G heads head0 .. head0 + G - 1 (one column group): lane (n, g) writes
+// head n, dims VD·(4g + e) .. +VD-1.
 template <int D, int NS>
-__device__ __forceinline__ void merge_states(const DecodeArgs& a, const float* rec, int rec_stride, int G,
-                                             int row, int head0, int tid, int nthreads) {
-  const int total4 = G * D / 4;
-  for (int e = tid; e < total4; e += nthreads) {
-    const int h = (e * 4) / D;
-    const int d = (e * 4) % D;
-    float M = kNegInf;
+__device__ __forceinline__ void merge_states(const DecodeArgs& a, const float* rec, int e, int G, int row,
+                                             int head0, int lane) {
+  constexpr int VD = D / 16;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  float M = kNegInf;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) M = fmaxf(M, rec[s * rec_stride + h]);
-    float L = 0.f;
-    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (M != kNegInf) {
+  for (int s = 0; s < NS; ++s) M = fmaxf(M, rec[s * kMergeRecFloats<D> + lane]);
+  float L = 0.f;
+  float o[VD];
 #pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const float* ws = rec + s * rec_stride;
-        const float wgt = fast_exp2(ws[h] - M);
-        L = __builtin_fmaf(ws[16 + h], wgt, L);
-        const float4 x = *reinterpret_cast<const float4*>(ws + 32 + h * D + d);
-        A.x = __builtin_fmaf(x.x, wgt, A.x);
-        A.y = __builtin_fmaf(x.y, wgt, A.y);
-        A.z = __builtin_fmaf(x.z, wgt, A.z);
-        A.w = __builtin_fmaf(x.w, wgt, A.w);
-      }
+  for (int c = 0; c < VD; ++c) o[c] = 0.f;
+  if (M != kNegInf) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const float* rs = rec + s * kMergeRecFloats<D>;
+      const float wgt = fast_exp2(rs[lane] - M);
+      L = __builtin_fmaf(rs[64 + lane], wgt, L);
+#pragma unroll
+      for (int c = 0; c < VD; ++c) o[c] = __builtin_fmaf(rs[128 + (64 * c + lane) * 4 + e], wgt, o[c]);
     }
-    const float inv = split_inv(L);
-    float4 o = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
-    if (L == 0.f) o = make_float4(0.f, 0.f, 0.f, 0.f);
-    const int head = head0 + h;
-    uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)row * a.o_sb + (int64_t)head * a.o_sh + d;
-    uint2 pk;
-    pk.x = pack_bf16x2_hw(o.x, o.y);
-    pk.y = pack_bf16x2_hw(o.z, o.w);
-    st8(dst, pk);
+  }
+  const float inv = split_inv(L);
+#pragma unroll
+  for (int c = 0; c < VD; ++c) o[c] = L == 0.f ? 0.f : o[c] * inv;
+  if (n < G) {
+    uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)row * a.o_sb + (int64_t)(head0 + n) * a.o_sh +
+                    VD * (4 * g + e);
+    if constexpr (VD == 8) {
+      uint4 pk;
+      pk.x = pack_bf16x2_hw(o[0], o[1]);
+      pk.y = pack_bf16x2_hw(o[2], o[3]);
+      pk.z = pack_bf16x2_hw(o[4], o[5]);
+      pk.w = pack_bf16x2_hw(o[6], o[7]);
+      st16(dst, pk);
+    } else {
+      uint2 pk;
+      pk.x = pack_bf16x2_hw(o[0], o[1]);
+      pk.y = pack_bf16x2_hw(o[2], o[3]);
+      st8(dst, pk);
+    }
   }
 }
 
 // LDS bytes one decode work-group uses: NW K transpose tiles, then NW merge
-// records of 32 + C·D floats, C = min(G, 16) heads per column group.
+// records.
 template <int D, int NW>
-constexpr size_t decode_lds_bytes(int G) {
-  return (size_t)NW * kTileBytes<D> + (size_t)NW * (32 + (G < 16 ? G : 16) * D) * sizeof(float);
+constexpr size_t decode_lds_bytes() {
+  return (size_t)NW * kTileBytes<D> + (size_t)NW * kMergeRecFloats<D> * sizeof(float);
 }
 
 // One single-pass decode work-group: (sequence, column group) = wg (a column
 // group is a KV head when G <= 16), with NW waves and `smem` pointing at
-// decode_lds_bytes<D, NW>(G) bytes of LDS. Wave w walks the row's pages w,
+// decode_lds_bytes<D, NW>() bytes of LDS. Wave w walks the row's pages w,
 // w + NW, ... with PF pages in flight; the NW states are merged in wave order
 // and the bf16 output rows are written.
 // EAGER (PF = 1): page k+1 is requested as soon as page k has landed, before
@@ -453,12 +457,14 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
     for (int i = 0; i < PF; ++i) wait_page<0, D>(r[i]);
   }
 
-  // Merge records (m[16], l[16], acc[G][D] per wave) follow the NW K tiles.
-  const int wstride = 32 + G * D;
+  // Every wave saves its state (the merge records follow the NW K tiles);
+  // then wave w merges element w of every lane's accumulator vectors and
+  // writes those dims of the output rows.
+  static_assert(NW == 4, "wave w merges element w of the 4-element accumulator vectors");
   float* merge = smem + NW * kTileBytes<D> / 4;
-  save_state<D>(merge + w * wstride, st, sum_across_groups(st.l), G, n, g);
+  save_state<D>(merge + w * kMergeRecFloats<D>, st, lane);
   __syncthreads();
-  merge_states<D, NW>(a, merge, wstride, G, row, cgp.head0, threadIdx.x, NW * 64);
+  merge_states<D, NW>(a, merge, w, G, row, cgp.head0, lane);
 }
 
 }  // namespace bvllm

@@ -118,7 +118,7 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
   // K tiles in buffers 0 and 1, V tiles in buffers 2 and 3.
   __shared__ __attribute__((aligned(1024))) unsigned char lds[4 * TB];
   static_assert(NW == kDecodeWaves, "decode work-groups run with the prefill work-group size");
-  static_assert(decode_lds_bytes<D, kDecodeWaves>(16) <= sizeof(lds), "decode work-group LDS");
+  static_assert(decode_lds_bytes<D, kDecodeWaves>() <= sizeof(lds), "decode work-group LDS");
 
   // The last n_dec_wgs work-groups are decode work-groups, one per (sequence,
   // KV head); those past the batch have nothing to do. They come after the
