@@ -243,19 +243,33 @@ __device__ __forceinline__ void process_page(WaveState<D>& st, const PageRegs<D>
 template <int D>
 constexpr int kTileBytes = 16 * (2 * D + 16);
 
-// A wave's final state as a merge record, per lane L = n + 16g: m at [L], the
-// row sum over the four lane groups (the same in all four) at [64 + L], then
-// accumulator vector c (head n, dims VD·(4g + i) + c for its elements i) at
-// [128 + 4·(64c + L)]: 16-byte stores in lane order, no LDS bank conflicts.
+// The 4 wave states of a work-group as merge records in LDS, laid out for the
+// reader: wave e merges element e of every lane's accumulator vectors, so
+// lane L of wave e finds everything it needs in two blocks it reads with
+// 16-byte loads and one wait:
+//   [8L .. 8L+8):            m of states 0..3, then their row sums (over the
+//                            four lane groups, the same in all four);
+//   [512 + (64e + L)·R ..):  element e of accumulator vector c of state s at
+//                            D/16·s + c (head n, dim D/16·(4g + e) + c;
+//                            L = n + 16g), the row padded to R floats so that
+//                            the 16-byte accesses of 16 lanes hit 64 banks.
 template <int D>
-constexpr int kMergeRecFloats = (2 + 4 * (D / 16)) * 64;
+constexpr int kMergeRowFloats = 4 * (D / 16) + 4;
+template <int D>
+constexpr int kMergeFloats = 64 * 8 + 4 * 64 * kMergeRowFloats<D>;
 
 template <int D>
-__device__ __forceinline__ void save_state(float* rec, const WaveState<D>& st, int lane) {
-  rec[lane] = st.m;
-  rec[64 + lane] = sum_across_groups(st.l);
+__device__ __forceinline__ void save_state(float* rec, const WaveState<D>& st, int s, int lane) {
+  constexpr int VD = D / 16;
+  rec[8 * lane + s] = st.m;
+  rec[8 * lane + 4 + s] = sum_across_groups(st.l);
 #pragma unroll
-  for (int c = 0; c < D / 16; ++c) *reinterpret_cast<f32x4_t*>(rec + 128 + (64 * c + lane) * 4) = st.acc[c];
+  for (int e = 0; e < 4; ++e) {
+    float* dst = rec + 512 + (64 * e + lane) * kMergeRowFloats<D> + VD * s;
+#pragma unroll
+    for (int c = 0; c < VD; c += 4)
+      *reinterpret_cast<f32x4_t*>(dst + c) = f32x4_t{st.acc[c][e], st.acc[c + 1][e], st.acc[c + 2][e], st.acc[c + 3][e]};
+  }
 }
 
 // Merge arithmetic of NS per-state results of one split, in state order:
@@ -268,32 +282,37 @@ __device__ __forceinline__ void save_state(float* rec, const WaveState<D>& st, i
 __device__ __forceinline__ float split_inv(float L) { return L > 0.f ? 1.f / L : 0.f; }
 __device__ __forceinline__ float split_lse(float M, float L) { return L > 0.f ? M + __log2f(L) : kNegInf; }
 
-// Merges the NS wave states of the row (one split: the single-pass launch) in
-// wave order (record s at rec + s·kMergeRecFloats) for element e of every
-// lane's accumulator vectors, and writes those dims of the bf16 output rows of
-// the G heads head0 .. head0 + G - 1 (one column group): lane (n, g) writes
-// head n, dims VD·(4g + e) .. +VD-1.
-template <int D, int NS>
+// Merges the 4 wave states of the row (one split: the single-pass launch) in
+// wave order for element e of every lane's accumulator vectors (records laid
+// out by save_state), and writes those dims of the bf16 output rows of the G
+// heads head0 .. head0 + G - 1 (one column group): lane (n, g) writes head n,
+// dims VD·(4g + e) .. +VD-1.
+template <int D>
 __device__ __forceinline__ void merge_states(const DecodeArgs& a, const float* rec, int e, int G, int row,
                                              int head0, int lane) {
   constexpr int VD = D / 16;
   const int n = lane & 15;
   const int g = lane >> 4;
+  const f32x4_t m4 = *reinterpret_cast<const f32x4_t*>(rec + 8 * lane);
+  const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(rec + 8 * lane + 4);
+  const float* row_e = rec + 512 + (64 * e + lane) * kMergeRowFloats<D>;
+  f32x4_t av[VD];  // 4 states x VD elements, state-major
+#pragma unroll
+  for (int k = 0; k < VD; ++k) av[k] = *reinterpret_cast<const f32x4_t*>(row_e + 4 * k);
   float M = kNegInf;
 #pragma unroll
-  for (int s = 0; s < NS; ++s) M = fmaxf(M, rec[s * kMergeRecFloats<D> + lane]);
+  for (int s = 0; s < 4; ++s) M = fmaxf(M, m4[s]);
   float L = 0.f;
   float o[VD];
 #pragma unroll
   for (int c = 0; c < VD; ++c) o[c] = 0.f;
   if (M != kNegInf) {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const float* rs = rec + s * kMergeRecFloats<D>;
-      const float wgt = fast_exp2(rs[lane] - M);
-      L = __builtin_fmaf(rs[64 + lane], wgt, L);
+    for (int s = 0; s < 4; ++s) {
+      const float wgt = fast_exp2(m4[s] - M);
+      L = __builtin_fmaf(l4[s], wgt, L);
 #pragma unroll
-      for (int c = 0; c < VD; ++c) o[c] = __builtin_fmaf(rs[128 + (64 * c + lane) * 4 + e], wgt, o[c]);
+      for (int c = 0; c < VD; ++c) o[c] = __builtin_fmaf(av[(VD * s + c) / 4][(VD * s + c) % 4], wgt, o[c]);
     }
   }
   const float inv = split_inv(L);
@@ -322,7 +341,8 @@ __device__ __forceinline__ void merge_states(const DecodeArgs& a, const float* r
 // records.
 template <int D, int NW>
 constexpr size_t decode_lds_bytes() {
-  return (size_t)NW * kTileBytes<D> + (size_t)NW * kMergeRecFloats<D> * sizeof(float);
+  static_assert(NW == 4, "the merge records hold four states");
+  return (size_t)NW * kTileBytes<D> + (size_t)kMergeFloats<D> * sizeof(float);
 }
 
 // One single-pass decode work-group: (sequence, column group) = wg (a column
@@ -462,9 +482,9 @@ __device__ __forceinline__ void decode_work_group(const DecodeArgs& a, const int
   // writes those dims of the output rows.
   static_assert(NW == 4, "wave w merges element w of the 4-element accumulator vectors");
   float* merge = smem + NW * kTileBytes<D> / 4;
-  save_state<D>(merge + w * kMergeRecFloats<D>, st, lane);
+  save_state<D>(merge, st, w, lane);
   __syncthreads();
-  merge_states<D, NW>(a, merge, w, G, row, cgp.head0, lane);
+  merge_states<D>(a, merge, w, G, row, cgp.head0, lane);
 }
 
 }  // namespace bvllm
