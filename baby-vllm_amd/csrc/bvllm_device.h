@@ -46,11 +46,6 @@ __device__ __forceinline__ uint32_t pack_bf16x2_hw(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// True when every active lane of the wave holds x == 1.
-__device__ __forceinline__ bool wave_all_one(float x) {
-  return __builtin_amdgcn_ballot_w64(x != 1.f) == 0;
-}
-
 // Low / high bf16 of a dword as float.
 __device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }

@@ -141,8 +141,11 @@ __device__ __forceinline__ f32x4_t page_scores(const uint4 (&kop)[D / 32], const
 // states can interleave their pages (a dependent VALU operation waits about
 // 36 clocks for its operand on gfx950, so one page alone is latency-bound):
 //   softmax_phase: scores, running max and sum, P, and the PV operands;
-//   rescale_phase: the accumulator rescale, skipped when alpha is 1 on every
-//                  lane (x·1 == x: skipping is exact);
+//   rescale_phase: the accumulator rescale, skipped when every lane has
+//                  alpha = 1 (x·1 == x) or a state that has seen no live
+//                  token (its accumulators are +0, and +0·alpha = +0): both
+//                  skips are exact, and the second saves a state's first page
+//                  after every reset (each split's start) the rescale;
 //   pv_phase:      the PV MFMAs.
 // Tokens at or past tok_limit are masked: their scores become -inf and their
 // V rows are replaced by zeros where they are used (unwritten slots may hold
@@ -151,6 +154,7 @@ __device__ __forceinline__ f32x4_t page_scores(const uint4 (&kop)[D / 32], const
 template <int D>
 struct PagePv {
   float alpha;
+  bool fresh;          // the state had seen no live token (m = -inf): its accumulators are +0
   uint2 pb;            // P, bf16, B operand of the PV MFMAs
   uint2 va[D / 16];    // V^T operands (row = dim (D/16)·r + c, k = token 4g+i)
 };
@@ -176,6 +180,7 @@ __device__ __forceinline__ void softmax_phase(WaveState<D>& st, PagePv<D>& ph, f
   // so that alpha and p are 0 instead of exp2(-inf - -inf) = NaN.
   const float m_ref = m_new == kNegInf ? 0.f : m_new;
   ph.alpha = fast_exp2(st.m - m_ref);
+  ph.fresh = st.m == kNegInf;
   float p[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) p[i] = fast_exp2(sv[i] - m_ref);
@@ -199,7 +204,7 @@ __device__ __forceinline__ void softmax_phase(WaveState<D>& st, PagePv<D>& ph, f
 
 template <int D>
 __device__ __forceinline__ void rescale_phase(WaveState<D>& st, const PagePv<D>& ph) {
-  if (!wave_all_one(ph.alpha)) {
+  if (__builtin_amdgcn_ballot_w64(ph.alpha != 1.f && !ph.fresh) != 0) {
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) st.acc[c] *= ph.alpha;
   }
