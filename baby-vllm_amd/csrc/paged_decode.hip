@@ -20,14 +20,14 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
   decode_work_group<D, NW, PF, EAGER>(a, blockIdx.x, smem);
 }
 
-// Two waves per split, or per group of splits (PAIR), four pages in flight each.
+// Two waves per split (four pages in flight each) or per group of splits (two).
 template <int D, bool NT, bool GROUP>
 __global__ __launch_bounds__(128) void paged_decode_pair_kernel(DecodeArgs a, int items) {
   __shared__ __attribute__((aligned(16))) unsigned char tile[2 * kTileBytes<D>];
   __shared__ __attribute__((aligned(16))) float xs[(GROUP ? 2 : 1) * kPairLdsFloats<D>];
   const int item = (int)blockIdx.x;
   if (item >= items) return;
-  decode_stream_wave<D, 4, NT, GROUP, true>(a, item, tile + wave_id() * kTileBytes<D>, xs);
+  decode_stream_wave<D, GROUP ? 2 : 4, NT, GROUP, true>(a, item, tile + wave_id() * kTileBytes<D>, xs);
 }
 
 // One streaming wave per work-group, so that a short batch's splits spread
@@ -282,12 +282,13 @@ DecodePlan decode_plan(int32_t batch, int32_t num_kv_heads, int32_t num_splits, 
   p.partials = group_mode ? (int32_t)groups : num_splits;
   p.fold_in_reduce = !group_mode && p.group > 1;
   // Two waves per work-group: for single splits unless knob 1; for groups of
-  // splits when the one-wave grid has at most one wave per CU, since the
-  // two-wave group kernel runs one wave per SIMD (2 x 8192 and 4 x 4096, 256
-  // groups: 22.3-22.6 -> 19.7-20.3 us; 1 x 32768, 512 groups: 25.6-25.9 against
-  // 25.2-25.4 us on one wave; 8 x 32768: 116-119 against 106 us).
+  // splits when there are at most two groups per CU (two waves per group, two
+  // pages in flight each, one wave per SIMD: 1 x 32768 and 2 x 16384, 512
+  // groups: 23.5 -> 21.5 and 24.1 -> 21.2 us; 4 x 4096, 256 groups: 22.0 ->
+  // 18.2 us), one wave per group beyond (8 x 16384, 1024 groups: 52.8 against
+  // 56.4 us on two waves; 4 x 32768, 2048 groups: 60.0 against 64.3 us).
   const int64_t group_items = (int64_t)batch * num_kv_heads * groups;
-  p.pair = group_mode ? (forced == 3 || (forced != 2 && group_items <= device_cus())) : forced != 1;
+  p.pair = group_mode ? (forced == 3 || (forced != 2 && group_items <= 2 * (int64_t)device_cus())) : forced != 1;
   return p;
 }
 

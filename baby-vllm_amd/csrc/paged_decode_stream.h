@@ -77,9 +77,10 @@ __device__ __forceinline__ float group_lse(const GroupFold& f) { return f.L > 0.
 // (kTileBytes<D> bytes of LDS).
 // PAIR: the item's work-group has two waves; wave w holds states 2w and 2w+1
 // of each split (its pages 4k + 2w and 4k + 2w + 1), with four pages in flight
-// instead of two, and hands its states to wave 0 through `xs` (kPairLdsFloats<D>
-// floats of LDS, twice that with GROUP) at the end of every split; wave 0
-// merges the four in order as a single wave would.
+// for a single split and two for a group of splits, and hands its states to
+// wave 0 through `xs` (kPairLdsFloats<D> floats of LDS, twice that with GROUP)
+// at the end of every split; wave 0 merges the four in order as a single wave
+// would.
 template <int D>
 constexpr int kPairLdsFloats = 2 * (2 + 4 * (D / 16)) * 64;
 
@@ -89,7 +90,7 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
   constexpr int KC = D / 32;
   constexpr int VD = D / 16;
   constexpr int OPL = D / 4;  // output floats per lane: head n, dims VD·(4g+i) + c
-  static_assert((!PAIR && PF == 2) || (PAIR && PF == 4), "pages in flight per wave");
+  static_assert(PF == (PAIR && !GROUP ? 4 : 2), "pages in flight per wave");
   const int w = PAIR ? wave_id() : 0;
 
   const int S = a.num_splits;
@@ -277,32 +278,70 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
     const int slot_ent = min(max(ent, 0), a.num_pages - 1);
     auto phys = [&](int k) -> int64_t { return (int64_t)__builtin_amdgcn_readlane(slot_ent, k); };
     PageRegs<D> r[PF];
+    if constexpr (PAIR && GROUP) {
+      // A group of splits on two waves: two pages in flight per wave, page
+      // k + 4 requested once page k is computed. The wave's pages in order:
+      // q = 4j + 2w + i for ring slot i, state i (global state 2w + i).
+      // (Four in flight, as in split mode, put 32 MB of requests in flight at
+      // B1 x 32768 and ran it in 24.3 us against 21.2.)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int64_t p = phys(min(2 * w + i, here - 1)) * a.c_sb;
+        load_page<D, NT>(r[i], kc + p, vc + p, off);
+      }
+      // At a split's first page: wave 1's states go to wave 0, which merges
+      // and folds the split that ended.
+      auto new_split = [&](int quad) __attribute__((always_inline)) {
+        if (quad < here && base + quad == next_start) {
+          pair_exchange(xb);
+          xb ^= 1;
+          if (w == 0) finish_split(cur);
+          ++cur;
+          next_start = (cur + 1 < j1) ? next_start + bps : INT_MAX;
+          any = false;
+        }
+      };
+      int k = 0;
+      for (; k + 4 < here; k += 4) {
+        new_split(k);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          wait_page<kLoadsPerPage, D>(r[i]);
+          const int q = k + 2 * w + i;
+          if (q < here)
+            process_page<D>(st[i], r[i], qb, tile, n, g, (p0 + base + q) * 16 + 4 * g, seq_len, a.scale_log2);
+          const int64_t pn = phys(min(q + 4, here - 1)) * a.c_sb;
+          load_page<D, NT>(r[i], kc + pn, vc + pn, off);
+        }
+        any = true;
+      }
+      // The last four pages: no load past them, and slot i waits for itself only.
+      new_split(k);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        if (i == 0) wait_page<kLoadsPerPage, D>(r[0]);
+        else wait_page<0, D>(r[1]);
+        const int q = k + 2 * w + i;
+        if (q < here)
+          process_page<D>(st[i], r[i], qb, tile, n, g, (p0 + base + q) * 16 + 4 * g, seq_len, a.scale_log2);
+      }
+      any = true;
+      continue;
+    }
     if constexpr (PAIR) {
-      // The wave's pages in order: q = 8j + 4(i/2) + 2w + (i mod 2) for ring
-      // slot i, state i mod 2 (global state 2w + i mod 2).
+      // Split mode on two waves, four pages in flight per wave: the wave's
+      // pages in order are q = 8j + 4(i/2) + 2w + (i mod 2) for ring slot i,
+      // state i mod 2 (global state 2w + i mod 2).
 #pragma unroll
       for (int i = 0; i < PF; ++i) {
         const int64_t p = phys(min(4 * (i >> 1) + 2 * w + (i & 1), here - 1)) * a.c_sb;
         load_page<D, NT>(r[i], kc + p, vc + p, off);
       }
-      auto new_split = [&](int i, int quad) __attribute__((always_inline)) {
-        if constexpr (GROUP) {
-          if ((i & 1) == 0 && quad < here && base + quad == next_start) {  // a new split starts here
-            pair_exchange(xb);
-            xb ^= 1;
-            if (w == 0) finish_split(cur);
-            ++cur;
-            next_start = (cur + 1 < j1) ? next_start + bps : INT_MAX;
-            any = false;
-          }
-        }
-      };
       int k = 0;
       for (; k + 8 < here; k += 8) {
 #pragma unroll
         for (int i = 0; i < PF; ++i) {
           const int quad = k + 4 * (i >> 1);  // first page of the 4-page block of slot i
-          new_split(i, quad);
           wait_page<(PF - 1) * kLoadsPerPage, D>(r[i]);
           const int q = quad + 2 * w + (i & 1);
           if (q < here)
@@ -314,12 +353,10 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
       }
       // The last eight pages (all of them when the chunk has at most eight, as
       // in a split of 8 pages): no load past them, and slot i waits for itself
-      // only (B8 x 1920: 15.6 -> 14.8 us; B1 x 32768 on two waves per group:
-      // 25.8 -> 25.1 us).
+      // only (B8 x 1920: 15.6 -> 14.8 us).
 #pragma unroll
       for (int i = 0; i < PF; ++i) {
         const int quad = k + 4 * (i >> 1);
-        new_split(i, quad);
         if (i == 0) wait_page<3 * kLoadsPerPage, D>(r[0]);
         else if (i == 1) wait_page<2 * kLoadsPerPage, D>(r[1]);
         else if (i == 2) wait_page<kLoadsPerPage, D>(r[2]);
