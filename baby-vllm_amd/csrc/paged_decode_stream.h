@@ -77,12 +77,15 @@ __device__ __forceinline__ float group_lse(const GroupFold& f) { return f.L > 0.
 // (kTileBytes<D> bytes of LDS).
 // PAIR: the item's work-group has two waves; wave w holds states 2w and 2w+1
 // of each split (its pages 4k + 2w and 4k + 2w + 1), with four pages in flight
-// for a single split and two for a group of splits, and hands its states to
-// wave 0 through `xs` (kPairLdsFloats<D> floats of LDS, twice that with GROUP)
-// at the end of every split; wave 0 merges the four in order as a single wave
-// would.
+// for a single split and two for a group of splits. At the end of every split
+// both waves publish their states through `xs` (kPairLdsFloats<D> floats of
+// LDS, twice that with GROUP), and wave w merges elements 2w and 2w + 1 of
+// every lane's accumulator vectors from the four, in order, as a single wave
+// would (and folds or writes those output dims).
 template <int D>
-constexpr int kPairLdsFloats = 2 * (2 + 4 * (D / 16)) * 64;
+constexpr int kPairRecFloats = (2 + 4 * (D / 16)) * 64;  // m, l, accumulators of one state, per lane
+template <int D>
+constexpr int kPairLdsFloats = 4 * kPairRecFloats<D>;
 
 template <int D, int PF, bool NT, bool GROUP, bool PAIR = false>
 __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const int item, unsigned char* tile,
@@ -158,15 +161,61 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
   };
   reset();
 
+  // The accumulator elements whose output dims this wave merges: all four
+  // (one wave), or 2w and 2w + 1 (two waves); o[VD·(i - i0) + c] holds
+  // element i of vector c (head n, dim VD·(4g + i) + c).
+  constexpr int NI = PAIR ? 2 : 4;
+  constexpr int OPW = NI * VD;
+  const int i0 = PAIR ? 2 * w : 0;
+
   // Group accumulator (level 2 in the wave; group waves only).
-  float go[GROUP ? OPL : 1];
+  float go[GROUP ? OPW : 1];
 #pragma unroll
-  for (int k = 0; k < (GROUP ? OPL : 1); ++k) go[k] = 0.f;
+  for (int k = 0; k < (GROUP ? OPW : 1); ++k) go[k] = 0.f;
   GroupFold gf;
 
   const int64_t head = (int64_t)cgp.head0 + n;
+  // Folds (group waves) or writes a split's (o, lse) for this wave's dims.
+  auto emit = [&](int split, float (&o)[OPW], float lse) __attribute__((always_inline)) {
+    if constexpr (GROUP) {
+      float wa, wb;
+      group_fold_weights(gf, lse, wa, wb);
+#pragma unroll
+      for (int k = 0; k < OPW; ++k) go[k] = group_fold_value(go[k], o[k], wa, wb);
+    } else if (n < G) {
+      if (S == 1) {
+        uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)b * a.o_sb + head * a.o_sh;
+#pragma unroll
+        for (int ii = 0; ii < NI; ++ii) {
+          if constexpr (VD == 8) {
+            uint4 pk;
+            pk.x = pack_bf16x2_hw(o[VD * ii + 0], o[VD * ii + 1]);
+            pk.y = pack_bf16x2_hw(o[VD * ii + 2], o[VD * ii + 3]);
+            pk.z = pack_bf16x2_hw(o[VD * ii + 4], o[VD * ii + 5]);
+            pk.w = pack_bf16x2_hw(o[VD * ii + 6], o[VD * ii + 7]);
+            st16(dst + VD * (4 * g + i0 + ii), pk);
+          } else {
+            uint2 pk;
+            pk.x = pack_bf16x2_hw(o[VD * ii + 0], o[VD * ii + 1]);
+            pk.y = pack_bf16x2_hw(o[VD * ii + 2], o[VD * ii + 3]);
+            st8(dst + VD * (4 * g + i0 + ii), pk);
+          }
+        }
+      } else {
+        const int64_t prow = ((int64_t)b * a.num_heads + head) * a.num_partials + split;
+        float* dst = a.part_out + prow * D;
+#pragma unroll
+        for (int ii = 0; ii < NI; ++ii)
+#pragma unroll
+          for (int c = 0; c < VD; c += 4)
+            *reinterpret_cast<float4*>(dst + VD * (4 * g + i0 + ii) + c) =
+                make_float4(o[VD * ii + c], o[VD * ii + c + 1], o[VD * ii + c + 2], o[VD * ii + c + 3]);
+        if (g == 0 && i0 == 0) a.part_lse[prow] = lse;
+      }
+    }
+  };
   // Merges the 4 states of split `split` (merge_states' arithmetic, per lane)
-  // and folds or writes its (o, lse).
+  // and folds or writes its (o, lse). One wave: the states in registers.
   auto finish_split = [&](int split) __attribute__((always_inline)) {
     float lt[4];
 #pragma unroll
@@ -192,76 +241,60 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
     const float inv = split_inv(L);
 #pragma unroll
     for (int k = 0; k < OPL; ++k) o[k] = L == 0.f ? 0.f : o[k] * inv;
-    const float lse = split_lse(M, L);
-    if constexpr (GROUP) {
-      float wa, wb;
-      group_fold_weights(gf, lse, wa, wb);
-#pragma unroll
-      for (int k = 0; k < OPL; ++k) go[k] = group_fold_value(go[k], o[k], wa, wb);
-    } else if (n < G) {
-      if (S == 1) {
-        uint16_t* dst = reinterpret_cast<uint16_t*>(a.out) + (int64_t)b * a.o_sb + head * a.o_sh;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if constexpr (VD == 8) {
-            uint4 pk;
-            pk.x = pack_bf16x2_hw(o[VD * i + 0], o[VD * i + 1]);
-            pk.y = pack_bf16x2_hw(o[VD * i + 2], o[VD * i + 3]);
-            pk.z = pack_bf16x2_hw(o[VD * i + 4], o[VD * i + 5]);
-            pk.w = pack_bf16x2_hw(o[VD * i + 6], o[VD * i + 7]);
-            st16(dst + VD * (4 * g + i), pk);
-          } else {
-            uint2 pk;
-            pk.x = pack_bf16x2_hw(o[VD * i + 0], o[VD * i + 1]);
-            pk.y = pack_bf16x2_hw(o[VD * i + 2], o[VD * i + 3]);
-            st8(dst + VD * (4 * g + i), pk);
-          }
-        }
-      } else {
-        const int64_t prow = ((int64_t)b * a.num_heads + head) * a.num_partials + split;
-        float* dst = a.part_out + prow * D;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int c = 0; c < VD; c += 4)
-            *reinterpret_cast<float4*>(dst + VD * (4 * g + i) + c) =
-                make_float4(o[VD * i + c], o[VD * i + c + 1], o[VD * i + c + 2], o[VD * i + c + 3]);
-        if (g == 0) a.part_lse[prow] = lse;
-      }
-    }
+    if constexpr (!PAIR) emit(split, o, split_lse(M, L));
     reset();
   };
 
-  // PAIR: wave 1's states become states 2 and 3 of wave 0, through LDS
-  // buffer xb (one barrier; both waves call it). Wave 1's states restart.
-  auto pair_exchange = [&](int xb) __attribute__((always_inline)) {
+  // PAIR: both waves publish their two states (records 2w and 2w + 1 of LDS
+  // buffer xb, global states 2w and 2w + 1) and restart them; after one
+  // barrier wave w merges elements i0, i0 + 1 of every lane's accumulator
+  // vectors from the four records, in state order, and folds or writes them.
+  auto pair_finish = [&](int xb, int split) __attribute__((always_inline)) {
     float* xbase = xs + xb * kPairLdsFloats<D>;
-    if (w == 1) {
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        float* rec = xbase + s2 * (2 + 4 * VD) * 64;
-        rec[lane] = st[s2].m;
-        rec[64 + lane] = st[s2].l;
+    for (int s2 = 0; s2 < 2; ++s2) {
+      float* rec = xbase + (2 * w + s2) * kPairRecFloats<D>;
+      rec[lane] = st[s2].m;
+      rec[64 + lane] = st[s2].l;
 #pragma unroll
-        for (int c = 0; c < VD; ++c) *reinterpret_cast<f32x4_t*>(rec + 128 + (c * 64 + lane) * 4) = st[s2].acc[c];
-      }
-      reset();
+      for (int c = 0; c < VD; ++c) *reinterpret_cast<f32x4_t*>(rec + 128 + (c * 64 + lane) * 4) = st[s2].acc[c];
     }
+    reset();
     __syncthreads();
-    if (w == 0) {
+    float mv[4], lt[4];
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const float* rec = xbase + s2 * (2 + 4 * VD) * 64;
-        st[2 + s2].m = rec[lane];
-        st[2 + s2].l = rec[64 + lane];
+    for (int s = 0; s < 4; ++s) {
+      mv[s] = xbase[s * kPairRecFloats<D> + lane];
+      lt[s] = sum_across_groups(xbase[s * kPairRecFloats<D> + 64 + lane]);
+    }
+    float M = kNegInf;
 #pragma unroll
-        for (int c = 0; c < VD; ++c)
-          st[2 + s2].acc[c] = *reinterpret_cast<const f32x4_t*>(rec + 128 + (c * 64 + lane) * 4);
+    for (int s = 0; s < 4; ++s) M = fmaxf(M, mv[s]);
+    float L = 0.f;
+    float o[OPW];
+#pragma unroll
+    for (int k = 0; k < OPW; ++k) o[k] = 0.f;
+    if (M != kNegInf) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float wgt = fast_exp2(mv[s] - M);
+        L = __builtin_fmaf(lt[s], wgt, L);
+        const float* racc = xbase + s * kPairRecFloats<D> + 128 + i0;
+#pragma unroll
+        for (int c = 0; c < VD; ++c) {
+          const float2 x = *reinterpret_cast<const float2*>(racc + (c * 64 + lane) * 4);
+          o[c] = __builtin_fmaf(x.x, wgt, o[c]);
+          o[VD + c] = __builtin_fmaf(x.y, wgt, o[VD + c]);
+        }
       }
     }
+    const float inv = split_inv(L);
+#pragma unroll
+    for (int k = 0; k < OPW; ++k) o[k] = L == 0.f ? 0.f : o[k] * inv;
+    emit(split, o, split_lse(M, L));
   };
-  int xb = 0;  // PAIR with GROUP: the exchange buffers alternate, so wave 1 never
-               // overwrites a record wave 0 has not read (a barrier lies between)
+  int xb = 0;  // PAIR with GROUP: the exchange buffers alternate, so no wave
+               // overwrites a record the other has not read (a barrier lies between)
 
   int cur = j0;  // split whose states are open
   // Item-relative page index where split cur + 1 starts (none past the unit).
@@ -289,13 +322,11 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
         const int64_t p = phys(min(2 * w + i, here - 1)) * a.c_sb;
         load_page<D, NT>(r[i], kc + p, vc + p, off);
       }
-      // At a split's first page: wave 1's states go to wave 0, which merges
-      // and folds the split that ended.
+      // At a split's first page: the split that ended is merged and folded.
       auto new_split = [&](int quad) __attribute__((always_inline)) {
         if (quad < here && base + quad == next_start) {
-          pair_exchange(xb);
+          pair_finish(xb, cur);
           xb ^= 1;
-          if (w == 0) finish_split(cur);
           ++cur;
           next_start = (cur + 1 < j1) ? next_start + bps : INT_MAX;
           any = false;
@@ -398,28 +429,27 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
 #pragma unroll
     for (int i = 0; i < PF; ++i) wait_page<0, D>(r[i]);
   }
-  if constexpr (PAIR) {
-    // The last split's states (both waves agree on `any`: it follows the
-    // 4-page blocks, not the pages each wave computed).
-    if (any || !GROUP) pair_exchange(xb);
-    if (w == 1) return;
-  }
   // The split holding the unit's last pages (for a unit of one split, also
-  // when it has no page: its partial is written as empty).
-  if (any || !GROUP) finish_split(cur);
+  // when it has no page: its partial is written as empty). Both waves of a
+  // pair agree on `any`: it follows the 4-page blocks, not the pages each
+  // wave computed.
+  if (any || !GROUP) {
+    if constexpr (PAIR) pair_finish(xb, cur);
+    else finish_split(cur);
+  }
 
   if (GROUP && n < G) {
     const int64_t prow = ((int64_t)b * a.num_heads + head) * a.num_partials + unit;
     float* dst = a.part_out + prow * D;
     const float ginv = group_inv(gf);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int ii = 0; ii < NI; ++ii)
 #pragma unroll
       for (int c = 0; c < VD; c += 4)
-        *reinterpret_cast<float4*>(dst + VD * (4 * g + i) + c) =
-            make_float4(go[VD * i + c] * ginv, go[VD * i + c + 1] * ginv, go[VD * i + c + 2] * ginv,
-                        go[VD * i + c + 3] * ginv);
-    if (g == 0) a.part_lse[prow] = group_lse(gf);
+        *reinterpret_cast<float4*>(dst + VD * (4 * g + i0 + ii) + c) =
+            make_float4(go[VD * ii + c] * ginv, go[VD * ii + c + 1] * ginv, go[VD * ii + c + 2] * ginv,
+                        go[VD * ii + c + 3] * ginv);
+    if (g == 0 && i0 == 0) a.part_lse[prow] = group_lse(gf);
   }
 }
 
