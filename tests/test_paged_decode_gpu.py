@@ -278,6 +278,23 @@ def test_launch_choices_do_not_change_bits(partition, lens, monkeypatch):
     assert_attn_close(outs["auto"], _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
 
 
+@pytest.mark.parametrize("hkv,group,d", [(2, 7, 64), (4, 7, 128), (1, 32, 128), (2, 24, 64)])
+@pytest.mark.parametrize("partition,bucket", [(8, 512), (4, 192), (5, 150), (4, 128), (16, 512), (4, 256)])
+def test_plans_of_two_to_four_splits(hkv, group, d, partition, bucket):
+    """Plans of 2-4 splits (the reduce folds groups of 4 splits when the pages
+    per split are a multiple of 4, not at 5): every launch choice gives the
+    same bits and the oracle's values, on rows of the bucket's length, of 0 and
+    1 tokens, and rows ending inside a split."""
+    lens = [bucket, 1, 0, bucket - 37, 17]
+    q, kv_cache, bt, seq_lens = make_decode_inputs(lens, width=cdiv(bucket, BLOCK_SIZE) + 1, seed=partition + bucket,
+                                                   hkv=hkv, group=group, d=d)
+    scale = d ** -0.5
+    outs = _modes(q, kv_cache, bt, seq_lens, scale, bucket, partition)
+    for name, out in outs.items():
+        assert torch.equal(out, outs["auto"]), name
+    assert_attn_close(outs["auto"], _oracle(q, kv_cache, bt, lens, scale), rows=_live(lens))
+
+
 @pytest.mark.parametrize("hkv,group,d", [(2, 7, 64), (1, 16, 128), (8, 4, 128), (4, 1, 64)])
 def test_launch_choices_other_head_configs(hkv, group, d):
     lens = [700, 33, 0, 1500]
