@@ -493,6 +493,20 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
     }
 #pragma unroll
     for (int ct = 0; ct < QT; ++ct) lsum[ct] = mfma_16x16x32(ones_bf16, pb[ct], lsum[ct]);
+    // Schedule: the transpose reads run four dim blocks ahead of the MFMAs
+    // that use them (8 reads, then per block its MFMAs and the next block's
+    // two reads). Left to itself the compiler issued them two blocks ahead in
+    // bursts, and every other block's MFMAs waited on LDS latency
+    // (1 x (2048+4096): 222.9 -> 216.5 us; two blocks ahead 220.3, six 216.5,
+    // all reads first 218.6; 64 x 128: 35.9 -> 35.2 us).
+    constexpr int kAhead = VD < 4 ? VD : 4;
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kAhead, 0);  // DS reads
+#pragma unroll
+    for (int c = 0; c < VD - kAhead; ++c) {
+      __builtin_amdgcn_sched_group_barrier(0x008, QT, 0);  // MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, (kAhead + 1) * QT, 0);
   };
   // Key split: the V operands of the wave's half (every dim block) are read
   // from LDS at the start of the tile step, before the next tile's QKᵀ, and a
