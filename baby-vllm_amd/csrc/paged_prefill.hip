@@ -612,6 +612,18 @@ __global__ __launch_bounds__(NW * 64, 2) void paged_prefill_kernel(PrefillArgs a
       __builtin_amdgcn_s_setprio(1);
       if (next) qk(Sn, kbuf_next, h_next);
       softmax_p(Sc, pb);
+      if constexpr (KS == 1 && !MB) {
+        // Schedule: the K reads, then each QKᵀ MFMA followed by one VALU
+        // instruction of P (1 x (2048+4096): 218.6 -> 214.9 us; two VALU per
+        // MFMA 215.4, three 230.3, the K reads spread between the MFMAs 230.2;
+        // the key-split step gains nothing measurable from the same groups).
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * KC, 0);  // DS reads
+#pragma unroll
+        for (int i = 0; i < 2 * KC * QT; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
+        }
+      }
       // P is formed here, under the QKᵀ MFMAs and beside the max, not sunk
       // past the branches below.
 #pragma unroll
