@@ -261,12 +261,22 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
     }
     reset();
     __syncthreads();
-    float mv[4], lt[4];
+    // Every read of the four records is issued before any is used: one wait
+    // (inside a branch around the sums they went out one or two at a time,
+    // each waited for).
+    float mv[4], lraw[4];
+    float2 xr[4][VD];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       mv[s] = xbase[s * kPairRecFloats<D> + lane];
-      lt[s] = sum_across_groups(xbase[s * kPairRecFloats<D> + 64 + lane]);
+      lraw[s] = xbase[s * kPairRecFloats<D> + 64 + lane];
+      const float* racc = xbase + s * kPairRecFloats<D> + 128 + i0;
+#pragma unroll
+      for (int c = 0; c < VD; ++c) xr[s][c] = *reinterpret_cast<const float2*>(racc + (c * 64 + lane) * 4);
     }
+    float lt[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) lt[s] = sum_across_groups(lraw[s]);
     float M = kNegInf;
 #pragma unroll
     for (int s = 0; s < 4; ++s) M = fmaxf(M, mv[s]);
@@ -274,18 +284,19 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
     float o[OPW];
 #pragma unroll
     for (int k = 0; k < OPW; ++k) o[k] = 0.f;
-    if (M != kNegInf) {
+    // No branch around the sums (a branch let the compiler sink the reads into
+    // it): with every state empty (M = -inf) the weights are 0 and so are
+    // the accumulators and sums, so L and o stay +0 as they would unsummed
+    // (B1 x 32768: 21.0 -> 20.7 us, B8 x 1920: 14.37 -> 14.20 us).
+    const bool live = M != kNegInf;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float wgt = fast_exp2(mv[s] - M);
-        L = __builtin_fmaf(lt[s], wgt, L);
-        const float* racc = xbase + s * kPairRecFloats<D> + 128 + i0;
+    for (int s = 0; s < 4; ++s) {
+      const float wgt = live ? fast_exp2(mv[s] - M) : 0.f;
+      L = __builtin_fmaf(lt[s], wgt, L);
 #pragma unroll
-        for (int c = 0; c < VD; ++c) {
-          const float2 x = *reinterpret_cast<const float2*>(racc + (c * 64 + lane) * 4);
-          o[c] = __builtin_fmaf(x.x, wgt, o[c]);
-          o[VD + c] = __builtin_fmaf(x.y, wgt, o[VD + c]);
-        }
+      for (int c = 0; c < VD; ++c) {
+        o[c] = __builtin_fmaf(xr[s][c].x, wgt, o[c]);
+        o[VD + c] = __builtin_fmaf(xr[s][c].y, wgt, o[VD + c]);
       }
     }
     const float inv = split_inv(L);
