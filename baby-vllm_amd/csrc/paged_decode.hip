@@ -20,16 +20,6 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeArgs a) {
   decode_work_group<D, NW, PF, EAGER>(a, blockIdx.x, smem);
 }
 
-// Two waves per split (four pages in flight each) or per group of splits (two).
-template <int D, bool NT, bool GROUP>
-__global__ __launch_bounds__(128) void paged_decode_pair_kernel(DecodeArgs a, int items) {
-  __shared__ __attribute__((aligned(16))) unsigned char tile[2 * kTileBytes<D>];
-  __shared__ __attribute__((aligned(16))) float xs[(GROUP ? 2 : 1) * kPairLdsFloats<D>];
-  const int item = (int)blockIdx.x;
-  if (item >= items) return;
-  decode_stream_wave<D, GROUP ? 2 : 4, NT, GROUP, true>(a, item, tile + wave_id() * kTileBytes<D>, xs);
-}
-
 // One streaming wave per work-group, so that a short batch's splits spread
 // over every CU.
 template <int D, int PF, bool NT, bool GROUP>
@@ -411,12 +401,19 @@ static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
   if (p.pair) {
     const bool group = a.splits_per_item > 1;
     const bool nt = tuning(kTuneDecodeCached) == 0;
-    const dim3 grid((unsigned)items), block(128);
-    if (group && nt) hipLaunchKernelGGL((paged_decode_pair_kernel<D, true, true>), grid, block, 0, stream, a, (int)items);
-    else if (group) hipLaunchKernelGGL((paged_decode_pair_kernel<D, false, true>), grid, block, 0, stream, a, (int)items);
-    else if (nt) hipLaunchKernelGGL((paged_decode_pair_kernel<D, true, false>), grid, block, 0, stream, a, (int)items);
-    else hipLaunchKernelGGL((paged_decode_pair_kernel<D, false, false>), grid, block, 0, stream, a, (int)items);
-    err = hipGetLastError();
+    err = hipErrorInvalidValue;
+    if constexpr (D == 128) {  // the D = 128 split walk (every other pair walk: paged_decode_pair.hip)
+      if (!group) {
+        const dim3 grid((unsigned)items), block(128);
+        if (nt) hipLaunchKernelGGL((paged_decode_pair_kernel<D, true, false>), grid, block, 0, stream, a, (int)items);
+        else hipLaunchKernelGGL((paged_decode_pair_kernel<D, false, false>), grid, block, 0, stream, a, (int)items);
+        err = hipGetLastError();
+      } else {
+        err = launch_pair_vgpr(a, items, group, nt, stream);
+      }
+    } else {
+      err = launch_pair_vgpr(a, items, group, nt, stream);
+    }
   } else if (a.splits_per_item > 1) {
     err = launch_stream<D, true>(a, items, stream);
   } else {

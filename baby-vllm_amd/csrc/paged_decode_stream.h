@@ -464,4 +464,22 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
   }
 }
 
+// Two waves per split (four pages in flight each) or per group of splits
+// (two). Each specialization is instantiated by one translation unit only:
+// paged_decode_pair.hip (built with the MFMA accumulators in VGPRs) launches
+// the group walks and the D = 64 split walk, paged_decode.hip the D = 128
+// split walk.
+template <int D, bool NT, bool GROUP>
+__global__ __launch_bounds__(128) void paged_decode_pair_kernel(DecodeArgs a, int items) {
+  __shared__ __attribute__((aligned(16))) unsigned char tile[2 * kTileBytes<D>];
+  __shared__ __attribute__((aligned(16))) float xs[(GROUP ? 2 : 1) * kPairLdsFloats<D>];
+  const int item = (int)blockIdx.x;
+  if (item >= items) return;
+  decode_stream_wave<D, GROUP ? 2 : 4, NT, GROUP, true>(a, item, tile + wave_id() * kTileBytes<D>, xs);
+}
+
+// Launches paged_decode_pair_kernel<D, nt, group> for the specializations
+// paged_decode_pair.hip holds (group walks, and split walks at D = 64).
+hipError_t launch_pair_vgpr(const DecodeArgs& a, int64_t items, bool group, bool nt, hipStream_t stream);
+
 }  // namespace bvllm
