@@ -11,8 +11,11 @@ Model: vector memory instructions enter one in-order queue per wave (on gfx9
 ``vmcnt`` counts loads and stores together and they retire in order);
 ``s_waitcnt vmcnt(N)`` retires the oldest entries until at most N remain. An
 instruction that names a destination register of an inline-asm load still in
-the queue is a hit. Every control-flow path is explored (a worklist over
-(basic block, queue state) pairs, with a per-block cap on distinct states).
+the queue is a hit. Every control-flow path is explored: a worklist over
+(basic block, queue state) pairs, with queue states kept from the oldest pending
+inline-asm load on (which changes no answer, see _canonical) so that loops reach a
+fixed point; the check raises rather than give up if a block's states exceed a cap,
+so a kernel that passes had every path explored.
 """
 
 from __future__ import annotations
@@ -79,8 +82,22 @@ def _blocks(asm: str, name: str):
     return blocks, succ
 
 
-def check_kernel(asm: str, name: str, max_states_per_block: int = 200) -> list[tuple[str, str]]:
-    """(block, instruction) pairs that touch a register of an inline-asm load still in flight."""
+def _canonical(q: list) -> tuple:
+    """The queue from its oldest pending inline-asm load on. Dropping older entries
+    changes no answer: a vmcnt(N) retires such a load when len(q) - N exceeds its
+    position, and removing k entries ahead of it lowers both sides by k. With no
+    inline-asm load pending, nothing in the queue matters."""
+    for i, e in enumerate(q):
+        if e[0]:
+            return tuple(q[i:])
+    return ()
+
+
+def check_kernel(asm: str, name: str, max_states_per_block: int = 4096) -> list[tuple[str, str]]:
+    """(block, instruction) pairs that touch a register of an inline-asm load still in flight.
+
+    Raises RuntimeError if a block's distinct queue states exceed max_states_per_block
+    (the exploration would be incomplete)."""
     blocks, succ = _blocks(asm, name)
     hits: set[tuple[str, str]] = set()
     seen: set = set()
@@ -88,15 +105,18 @@ def check_kernel(asm: str, name: str, max_states_per_block: int = 200) -> list[t
     work = [("entry", ())]
     while work:
         b, queue = work.pop()
-        if (b, queue) in seen or per_block.get(b, 0) >= max_states_per_block:
+        if (b, queue) in seen:
             continue
-        seen.add((b, queue))
         per_block[b] = per_block.get(b, 0) + 1
+        if per_block[b] > max_states_per_block:
+            raise RuntimeError(f"{name}: more than {max_states_per_block} queue states at {b}")
+        seen.add((b, queue))
         q = list(queue)  # entries: (is an inline-asm load, its destination registers)
         for s, in_asm in blocks[b]:
             m = _VMCNT.match(s)
             if m:
                 del q[:max(0, len(q) - int(m.group(1)))]
+                q = list(_canonical(q))
                 continue
             if s.startswith("s_waitcnt"):
                 continue
@@ -108,6 +128,7 @@ def check_kernel(asm: str, name: str, max_states_per_block: int = 200) -> list[t
                 writes_regs = "load" in op and "_lds_" not in op
                 dst = frozenset(registers(rest.split(",")[0])) if writes_regs else frozenset()
                 q.append((in_asm and writes_regs, dst))
+                q = list(_canonical(q))
         for nb in succ[b]:
             work.append((nb, tuple(q)))
     return sorted(hits)
