@@ -279,6 +279,8 @@ DecodePlan decode_plan(int32_t batch, int32_t num_kv_heads, int32_t num_splits, 
   // 56.4 us on two waves; 4 x 32768, 2048 groups: 60.0 against 64.3 us).
   const int64_t group_items = (int64_t)batch * num_kv_heads * groups;
   p.pair = group_mode ? (forced == 3 || (forced != 2 && group_items <= 2 * (int64_t)device_cus())) : forced != 1;
+  // Four waves per split when a split has at most 8 pages (two per wave), unless knob 4.
+  p.quad = p.pair && !group_mode && blocks_per_split <= 8 && forced != 4;
   return p;
 }
 
@@ -398,7 +400,14 @@ static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
   const int64_t items = (int64_t)a.batch * decode_col_groups(a) * units;
   if (items > 0x7ffffff0) return hipErrorInvalidValue;
   hipError_t err;
-  if (p.pair) {
+  if (p.quad) {
+    const dim3 grid((unsigned)items);
+    if (tuning(kTuneDecodeCached) == 0)
+      hipLaunchKernelGGL((paged_decode_quad_kernel<D, true>), grid, dim3(256), 0, stream, a, (int)items);
+    else
+      hipLaunchKernelGGL((paged_decode_quad_kernel<D, false>), grid, dim3(256), 0, stream, a, (int)items);
+    err = hipGetLastError();
+  } else if (p.pair) {
     const bool group = a.splits_per_item > 1;
     const bool nt = tuning(kTuneDecodeCached) == 0;
     err = hipErrorInvalidValue;

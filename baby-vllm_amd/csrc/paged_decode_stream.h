@@ -82,18 +82,24 @@ __device__ __forceinline__ float group_lse(const GroupFold& f) { return f.L > 0.
 // LDS, twice that with GROUP), and wave w merges elements 2w and 2w + 1 of
 // every lane's accumulator vectors from the four, in order, as a single wave
 // would (and folds or writes those output dims).
+// QUAD (with PAIR, single splits of at most 8 pages): four waves; wave w holds
+// state w (its pages w and 4 + w, both in flight from the start), publishes
+// it at the split's end, and merges element w of every accumulator vector from
+// the four records: the same arithmetic in the same order, on a quarter of the
+// pages and dims per wave.
 template <int D>
 constexpr int kPairRecFloats = (2 + 4 * (D / 16)) * 64;  // m, l, accumulators of one state, per lane
 template <int D>
 constexpr int kPairLdsFloats = 4 * kPairRecFloats<D>;
 
-template <int D, int PF, bool NT, bool GROUP, bool PAIR = false>
+template <int D, int PF, bool NT, bool GROUP, bool PAIR = false, bool QUAD = false>
 __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const int item, unsigned char* tile,
                                                    float* xs = nullptr) {
   constexpr int KC = D / 32;
   constexpr int VD = D / 16;
   constexpr int OPL = D / 4;  // output floats per lane: head n, dims VD·(4g+i) + c
-  static_assert(PF == (PAIR && !GROUP ? 4 : 2), "pages in flight per wave");
+  static_assert(PF == (PAIR && !GROUP && !QUAD ? 4 : 2), "pages in flight per wave");
+  static_assert(!QUAD || (PAIR && !GROUP), "four waves per item: single splits only");
   const int w = PAIR ? wave_id() : 0;
 
   const int S = a.num_splits;
@@ -162,11 +168,11 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
   reset();
 
   // The accumulator elements whose output dims this wave merges: all four
-  // (one wave), or 2w and 2w + 1 (two waves); o[VD·(i - i0) + c] holds
+  // (one wave), 2w and 2w + 1 (two waves) or w (four); o[VD·(i - i0) + c] holds
   // element i of vector c (head n, dim VD·(4g + i) + c).
-  constexpr int NI = PAIR ? 2 : 4;
+  constexpr int NI = QUAD ? 1 : PAIR ? 2 : 4;
   constexpr int OPW = NI * VD;
-  const int i0 = PAIR ? 2 * w : 0;
+  const int i0 = NI * w;
 
   // Group accumulator (level 2 in the wave; group waves only).
   float go[GROUP ? OPW : 1];
@@ -249,11 +255,14 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
   // buffer xb, global states 2w and 2w + 1) and restart them; after one
   // barrier wave w merges elements i0, i0 + 1 of every lane's accumulator
   // vectors from the four records, in state order, and folds or writes them.
+  // QUAD: each of the four waves publishes its one state (record w) and
+  // merges element w.
   auto pair_finish = [&](int xb, int split) __attribute__((always_inline)) {
     float* xbase = xs + xb * kPairLdsFloats<D>;
+    constexpr int SPW = QUAD ? 1 : 2;  // states per wave
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      float* rec = xbase + (2 * w + s2) * kPairRecFloats<D>;
+    for (int s2 = 0; s2 < SPW; ++s2) {
+      float* rec = xbase + (SPW * w + s2) * kPairRecFloats<D>;
       rec[lane] = st[s2].m;
       rec[64 + lane] = st[s2].l;
 #pragma unroll
@@ -265,14 +274,22 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
     // (inside a branch around the sums they went out one or two at a time,
     // each waited for).
     float mv[4], lraw[4];
-    float2 xr[4][VD];
+    float xr[4][VD][NI];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       mv[s] = xbase[s * kPairRecFloats<D> + lane];
       lraw[s] = xbase[s * kPairRecFloats<D> + 64 + lane];
       const float* racc = xbase + s * kPairRecFloats<D> + 128 + i0;
 #pragma unroll
-      for (int c = 0; c < VD; ++c) xr[s][c] = *reinterpret_cast<const float2*>(racc + (c * 64 + lane) * 4);
+      for (int c = 0; c < VD; ++c) {
+        if constexpr (NI == 2) {
+          const float2 x2 = *reinterpret_cast<const float2*>(racc + (c * 64 + lane) * 4);
+          xr[s][c][0] = x2.x;
+          xr[s][c][1] = x2.y;
+        } else {
+          xr[s][c][0] = racc[(c * 64 + lane) * 4];
+        }
+      }
     }
     float lt[4];
 #pragma unroll
@@ -295,8 +312,8 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
       L = __builtin_fmaf(lt[s], wgt, L);
 #pragma unroll
       for (int c = 0; c < VD; ++c) {
-        o[c] = __builtin_fmaf(xr[s][c].x, wgt, o[c]);
-        o[VD + c] = __builtin_fmaf(xr[s][c].y, wgt, o[VD + c]);
+#pragma unroll
+        for (int ii = 0; ii < NI; ++ii) o[VD * ii + c] = __builtin_fmaf(xr[s][c][ii], wgt, o[VD * ii + c]);
       }
     }
     const float inv = split_inv(L);
@@ -368,6 +385,35 @@ __device__ __forceinline__ void decode_stream_wave(const DecodeArgs& a, const in
           process_page<D>(st[i], r[i], qb, tile, n, g, (p0 + base + q) * 16 + 4 * g, seq_len, a.scale_log2);
       }
       any = true;
+      continue;
+    }
+    if constexpr (QUAD) {
+      // Split mode on four waves, two pages in flight per wave: the wave's
+      // pages in order are q = 8j + 4i + w for ring slot i, all of state w.
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        const int64_t p = phys(min(4 * i + w, here - 1)) * a.c_sb;
+        load_page<D, NT>(r[i], kc + p, vc + p, off);
+      }
+      int k = 0;
+      for (; k + 8 < here; k += 8) {
+#pragma unroll
+        for (int i = 0; i < PF; ++i) {
+          wait_page<(PF - 1) * kLoadsPerPage, D>(r[i]);
+          const int q = k + 4 * i + w;
+          if (q < here)
+            process_page<D>(st[0], r[i], qb, tile, n, g, (p0 + base + q) * 16 + 4 * g, seq_len, a.scale_log2);
+          const int64_t pn = phys(min(q + 8, here - 1)) * a.c_sb;
+          load_page<D, NT>(r[i], kc + pn, vc + pn, off);
+        }
+      }
+      // The last eight pages: no load past them, and slot i waits for itself only.
+      wait_page<kLoadsPerPage, D>(r[0]);
+      if (k + w < here)
+        process_page<D>(st[0], r[0], qb, tile, n, g, (p0 + base + k + w) * 16 + 4 * g, seq_len, a.scale_log2);
+      wait_page<0, D>(r[1]);
+      if (k + 4 + w < here)
+        process_page<D>(st[0], r[1], qb, tile, n, g, (p0 + base + k + 4 + w) * 16 + 4 * g, seq_len, a.scale_log2);
       continue;
     }
     if constexpr (PAIR) {
@@ -476,6 +522,19 @@ __global__ __launch_bounds__(128) void paged_decode_pair_kernel(DecodeArgs a, in
   const int item = (int)blockIdx.x;
   if (item >= items) return;
   decode_stream_wave<D, GROUP ? 2 : 4, NT, GROUP, true>(a, item, tile + wave_id() * kTileBytes<D>, xs);
+}
+
+// Four waves per single split of at most 8 pages (one state each, two pages
+// in flight): B8 x 1920 (15 splits of 8 pages) 14.3 -> 13.9 us and config 1
+// (4 of 8) 11.13 -> 10.85 us per layer against two waves per split. Both
+// specializations are instantiated by paged_decode.hip.
+template <int D, bool NT>
+__global__ __launch_bounds__(256) void paged_decode_quad_kernel(DecodeArgs a, int items) {
+  __shared__ __attribute__((aligned(16))) unsigned char tile[4 * kTileBytes<D>];
+  __shared__ __attribute__((aligned(16))) float xs[kPairLdsFloats<D>];
+  const int item = (int)blockIdx.x;
+  if (item >= items) return;
+  decode_stream_wave<D, 2, NT, false, true, true>(a, item, tile + wave_id() * kTileBytes<D>, xs);
 }
 
 // Launches paged_decode_pair_kernel<D, nt, group> for the specializations

@@ -82,7 +82,7 @@ def test_workspace_bytes_ignore_the_split_mode_knob():
     plans = [(8, 15, 8), (64, 2, 60), (16, 8, 16), (1, 512, 4), (2, 40, 8), (4, 20, 4), (1, 7, 5)]
     want = {p: h.bvllm_decode_workspace_bytes(p[0], 28, 4, 128, p[1], p[2]) for p in plans}
     try:
-        for knob_value in (1, 2, 3):
+        for knob_value in (1, 2, 3, 4):
             mod.set_tuning(mod.TUNE_DECODE_SPLIT_MODE, knob_value)
             for p in plans:
                 assert h.bvllm_decode_workspace_bytes(p[0], 28, 4, 128, p[1], p[2]) == want[p], (knob_value, p)

@@ -237,14 +237,16 @@ def test_reduce_bits_do_not_depend_on_the_split_count(n, monkeypatch):
 
 def _modes(q, kv_cache, bt, seq_lens, scale, bucket, partition):
     """Outputs of every launch choice that must give the same bits: split mode
-    (two waves per split by default, one wave per split, one or two waves per
-    group of 4 splits), wave order, nontemporal page loads, single pass on
-    streaming waves."""
+    (four waves per split of at most 8 pages and two per longer split by
+    default, two waves per split throughout, one wave per split, one or two
+    waves per group of 4 splits), wave order, nontemporal page loads, single
+    pass on streaming waves."""
     from babyvllm.kernels import _lib
 
     outs = {}
     choices = [("auto", None, 0), ("per_split", _lib.TUNE_DECODE_SPLIT_MODE, 1),
                ("per_group", _lib.TUNE_DECODE_SPLIT_MODE, 2), ("pair_group", _lib.TUNE_DECODE_SPLIT_MODE, 3),
+               ("pair_split", _lib.TUNE_DECODE_SPLIT_MODE, 4),
                ("order1", _lib.TUNE_DECODE_ORDER, 1), ("cached", _lib.TUNE_DECODE_CACHED, 1),
                ("stream_single", _lib.TUNE_DECODE_SINGLE_PASS_STREAM, 1)]
     for name, knob, value in choices:

@@ -32,7 +32,8 @@ _SPLIT_MODE, _BPW, _ORDER, _CACHED, _SHORT_GRID = 0, 1, 2, 4, 6  # bvllm_set_tun
 
 _DECODE_HEADS = [(4, 7, 128), (2, 7, 64), (8, 4, 128), (1, 16, 128), (4, 1, 64), (1, 32, 128), (2, 24, 64),
                  (1, 64, 128)]
-_DECODE_CHOICES = [None, (_SPLIT_MODE, 1), (_SPLIT_MODE, 2), (_SPLIT_MODE, 3), (_ORDER, 1), (_CACHED, 1)]
+_DECODE_CHOICES = [None, (_SPLIT_MODE, 1), (_SPLIT_MODE, 2), (_SPLIT_MODE, 3), (_SPLIT_MODE, 4), (_ORDER, 1),
+                   (_CACHED, 1)]
 
 
 def _decode_case(rng):
