@@ -401,12 +401,16 @@ static hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream) {
   if (items > 0x7ffffff0) return hipErrorInvalidValue;
   hipError_t err;
   if (p.quad) {
-    const dim3 grid((unsigned)items);
-    if (tuning(kTuneDecodeCached) == 0)
-      hipLaunchKernelGGL((paged_decode_quad_kernel<D, true>), grid, dim3(256), 0, stream, a, (int)items);
-    else
-      hipLaunchKernelGGL((paged_decode_quad_kernel<D, false>), grid, dim3(256), 0, stream, a, (int)items);
-    err = hipGetLastError();
+    if constexpr (D == 64) {
+      err = launch_quad_vgpr(a, items, tuning(kTuneDecodeCached) == 0, stream);
+    } else {
+      const dim3 grid((unsigned)items);
+      if (tuning(kTuneDecodeCached) == 0)
+        hipLaunchKernelGGL((paged_decode_quad_kernel<D, true>), grid, dim3(256), 0, stream, a, (int)items);
+      else
+        hipLaunchKernelGGL((paged_decode_quad_kernel<D, false>), grid, dim3(256), 0, stream, a, (int)items);
+      err = hipGetLastError();
+    }
   } else if (p.pair) {
     const bool group = a.splits_per_item > 1;
     const bool nt = tuning(kTuneDecodeCached) == 0;

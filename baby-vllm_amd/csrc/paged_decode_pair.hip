@@ -5,7 +5,8 @@
 // -mllvm -amdgpu-mfma-vgpr-form. Measured against the same kernels built with
 // AGPR accumulators: B1 x 32768 (group walk) 20.85 -> 20.55 us, config 1
 // (D = 64 split walk) 11.28 -> 11.13 us; the D = 128 split walk (B8 x 1920)
-// ran 14.38 -> 14.57 us that way and stays in paged_decode.hip.
+// ran 14.38 -> 14.57 us that way and stays in paged_decode.hip. The four-wave
+// split walk at D = 64 lives here too (config 1 10.76 -> 10.68 us).
 #include "paged_decode_stream.h"
 
 namespace bvllm {
@@ -29,6 +30,16 @@ hipError_t launch_pair_vgpr(const DecodeArgs& a, int64_t items, bool group, bool
     case 64: return launch_pair_dim<64>(a, items, group, nt, stream);
     case 128: return launch_pair_dim<128>(a, items, group, nt, stream);
     default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_quad_vgpr(const DecodeArgs& a, int64_t items, bool nt, hipStream_t stream) {
+  switch (a.head_dim) {
+    case 64:
+      if (nt) hipLaunchKernelGGL((paged_decode_quad_kernel<64, true>), dim3((unsigned)items), dim3(256), 0, stream, a, (int)items);
+      else hipLaunchKernelGGL((paged_decode_quad_kernel<64, false>), dim3((unsigned)items), dim3(256), 0, stream, a, (int)items);
+      return hipGetLastError();
+    default: return hipErrorInvalidValue;  // D = 128 launches from paged_decode.hip
   }
 }
 

@@ -526,8 +526,10 @@ __global__ __launch_bounds__(128) void paged_decode_pair_kernel(DecodeArgs a, in
 
 // Four waves per single split of at most 8 pages (one state each, two pages
 // in flight): B8 x 1920 (15 splits of 8 pages) 14.3 -> 13.9 us and config 1
-// (4 of 8) 11.13 -> 10.85 us per layer against two waves per split. Both
-// specializations are instantiated by paged_decode.hip.
+// (4 of 8) 11.13 -> 10.85 us per layer against two waves per split. D = 128
+// is instantiated by paged_decode.hip, D = 64 by paged_decode_pair.hip (with
+// VGPR accumulators: config 1 10.76 -> 10.68 us; D = 128 that way 13.97 ->
+// 14.04 us at B8).
 template <int D, bool NT>
 __global__ __launch_bounds__(256) void paged_decode_quad_kernel(DecodeArgs a, int items) {
   __shared__ __attribute__((aligned(16))) unsigned char tile[4 * kTileBytes<D>];
@@ -540,5 +542,7 @@ __global__ __launch_bounds__(256) void paged_decode_quad_kernel(DecodeArgs a, in
 // Launches paged_decode_pair_kernel<D, nt, group> for the specializations
 // paged_decode_pair.hip holds (group walks, and split walks at D = 64).
 hipError_t launch_pair_vgpr(const DecodeArgs& a, int64_t items, bool group, bool nt, hipStream_t stream);
+// Launches paged_decode_quad_kernel<64, nt> (held by paged_decode_pair.hip).
+hipError_t launch_quad_vgpr(const DecodeArgs& a, int64_t items, bool nt, hipStream_t stream);
 
 }  // namespace bvllm
