@@ -110,7 +110,7 @@ struct DecodePlan {
   int32_t partials;        // partial states per (row, head) in the workspace
   bool fold_in_reduce;     // the reduce folds the per-split partials into groups
   bool pair;               // one split or group per work-group of two waves (two states each)
-  bool quad;               // (with pair) one split of at most 8 pages per work-group of four waves
+  bool quad;               // (with pair) one split of at most 32 pages per work-group of four waves
 };
 DecodePlan decode_plan(int32_t batch, int32_t num_kv_heads, int32_t num_splits, int32_t blocks_per_split);
 // Column groups of a decode launch: its KV heads, each cut into ceil(G / 16)
@@ -127,8 +127,8 @@ int32_t decode_partials(int32_t batch, int32_t num_kv_heads, int32_t num_splits,
 enum TuneKnob {
   kTuneDecodeSplitMode = 0,         // 1: one wave per split, 2: one wave per group of splits, 3: two
                                     // waves per group, 4: two waves per split also for splits of at most
-                                    // 8 pages (same bits); by default single splits run on four waves
-                                    // (at most 8 pages) or two, groups on two waves when at most one
+                                    // 32 pages (same bits); by default single splits run on four waves
+                                    // (at most 32 pages) or two, groups on two waves when at most one
                                     // group per CU
   kTunePrefillBlocksPerWg = 1,      // n > 0: prefill column blocks per work-group when the table allows it
   kTuneDecodeOrder = 2,             // 1: split units fastest in the streaming wave numbering (same bits)

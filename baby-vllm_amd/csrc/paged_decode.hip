@@ -279,8 +279,8 @@ DecodePlan decode_plan(int32_t batch, int32_t num_kv_heads, int32_t num_splits, 
   // 56.4 us on two waves; 4 x 32768, 2048 groups: 60.0 against 64.3 us).
   const int64_t group_items = (int64_t)batch * num_kv_heads * groups;
   p.pair = group_mode ? (forced == 3 || (forced != 2 && group_items <= 2 * (int64_t)device_cus())) : forced != 1;
-  // Four waves per split when a split has at most 8 pages (two per wave), unless knob 4.
-  p.quad = p.pair && !group_mode && blocks_per_split <= 8 && forced != 4;
+  // Four waves per split when a split has at most 32 pages (at most 8 per wave), unless knob 4.
+  p.quad = p.pair && !group_mode && blocks_per_split <= 32 && forced != 4;
   return p;
 }
 

@@ -82,8 +82,8 @@ __device__ __forceinline__ float group_lse(const GroupFold& f) { return f.L > 0.
 // LDS, twice that with GROUP), and wave w merges elements 2w and 2w + 1 of
 // every lane's accumulator vectors from the four, in order, as a single wave
 // would (and folds or writes those output dims).
-// QUAD (with PAIR, single splits of at most 8 pages): four waves; wave w holds
-// state w (its pages w and 4 + w, both in flight from the start), publishes
+// QUAD (with PAIR, single splits of at most 32 pages): four waves; wave w holds
+// state w (its pages 4k + w, two in flight), publishes
 // it at the split's end, and merges element w of every accumulator vector from
 // the four records: the same arithmetic in the same order, on a quarter of the
 // pages and dims per wave.
@@ -524,9 +524,11 @@ __global__ __launch_bounds__(128) void paged_decode_pair_kernel(DecodeArgs a, in
   decode_stream_wave<D, GROUP ? 2 : 4, NT, GROUP, true>(a, item, tile + wave_id() * kTileBytes<D>, xs);
 }
 
-// Four waves per single split of at most 8 pages (one state each, two pages
-// in flight): B8 x 1920 (15 splits of 8 pages) 14.3 -> 13.9 us and config 1
-// (4 of 8) 11.13 -> 10.85 us per layer against two waves per split. D = 128
+// Four waves per single split of at most 32 pages (one state each, two pages
+// in flight): B8 x 1920 (15 splits of 8 pages) 14.3 -> 13.9 us, config 1 (4 of
+// 8) 11.13 -> 10.85 us, B8 x 4096 (32 of 8) 25.0 -> 23.0 us, B16 x 1920 (8 of
+// 16) 19.3 -> 18.6 us, B16 x 4096 (16 of 16) 34.1 -> 31.5 us, B32 x 1920 (4 of
+// 32) 29.3 -> 28.8 us per layer against two waves per split. D = 128
 // is instantiated by paged_decode.hip, D = 64 by paged_decode_pair.hip (with
 // VGPR accumulators: config 1 10.76 -> 10.68 us; D = 128 that way 13.97 ->
 // 14.04 us at B8).

@@ -183,7 +183,7 @@ BVLLM_API int bvllm_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_s
  * Tuning switch for experiments and tests (no counterpart in the reference):
  * sets process-wide knob `knob` to `value` (0 = the library's default) and
  * returns the previous value, or -1 for an unknown knob. Knobs: 0 decode split
- * mode (default: four waves per split of at most 8 pages, two per longer
+ * mode (default: four waves per split of at most 32 pages, two per longer
  * split, or per group of 4 splits when the plan groups them, two only while
  * the groups are at most one per compute unit; 1 one wave per split, 2 one
  * wave per group, 3 two waves per group, 4 two waves per split), 1 prefill

@@ -237,7 +237,7 @@ def test_reduce_bits_do_not_depend_on_the_split_count(n, monkeypatch):
 
 def _modes(q, kv_cache, bt, seq_lens, scale, bucket, partition):
     """Outputs of every launch choice that must give the same bits: split mode
-    (four waves per split of at most 8 pages and two per longer split by
+    (four waves per split of at most 32 pages and two per longer split by
     default, two waves per split throughout, one wave per split, one or two
     waves per group of 4 splits), wave order, nontemporal page loads, single
     pass on streaming waves."""
