@@ -528,7 +528,8 @@ __global__ __launch_bounds__(128) void paged_decode_pair_kernel(DecodeArgs a, in
 // in flight): B8 x 1920 (15 splits of 8 pages) 14.3 -> 13.9 us, config 1 (4 of
 // 8) 11.13 -> 10.85 us, B8 x 4096 (32 of 8) 25.0 -> 23.0 us, B16 x 1920 (8 of
 // 16) 19.3 -> 18.6 us, B16 x 4096 (16 of 16) 34.1 -> 31.5 us, B32 x 1920 (4 of
-// 32) 29.3 -> 28.8 us per layer against two waves per split. D = 128
+// 32) 29.3 -> 28.8 us, B24 x 4096 (8 of 32) 47.2 -> 40.9 us per layer against
+// two waves per split. D = 128
 // is instantiated by paged_decode.hip, D = 64 by paged_decode_pair.hip (with
 // VGPR accumulators: config 1 10.76 -> 10.68 us; D = 128 that way 13.97 ->
 // 14.04 us at B8).
